@@ -1,0 +1,145 @@
+/*
+ * treeattn_amd.h -- C ABI of the MI355X (gfx950) stochastic tree-attention library.
+ *
+ * Plain C: pointers, sizes and a HIP stream.  No torch types cross this
+ * boundary.  The caller allocates every buffer (outputs, the saved record and
+ * the workspaces, sized by the *_bytes queries below); the library never
+ * allocates, frees or synchronizes, and launches only on the stream it is
+ * given.  Every entry point returns TA_OK or an error code; the message of the
+ * last error on the calling thread is available from ta_last_error().
+ *
+ * Tensors q/k/v/out/dq/dk/dv are 4-D with the last (head) dimension
+ * contiguous; their other three strides (batch, position, head) are given in
+ * elements, so both the adapters' bshd layout (B,L,H,D) and the op-level
+ * (L,B,H,D) layout are read in place.
+ *
+ * Reference interfaces (paths under the reference repository):
+ *   packages/treeattn-cuda/csrc/treeattn_cuda.cpp          (pybind entry points)
+ *   packages/treeattn-cuda/src/treeattn_cuda/_autograd.py   (autograd Function)
+ *   packages/attn-bench/src/attn_bench/baselines/_treeattn_common.py (Haar keys)
+ */
+#ifndef TREEATTN_AMD_H
+#define TREEATTN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TA_VERSION 1
+
+/* return codes */
+#define TA_OK 0
+#define TA_ERR_INVALID 1      /* bad shape / option / pointer */
+#define TA_ERR_UNSUPPORTED 2  /* valid request outside what the kernels implement */
+#define TA_ERR_LAUNCH 3       /* HIP launch error */
+
+/* element types of q/k/v/out and their gradients */
+#define TA_F32 0
+#define TA_BF16 1
+#define TA_F16 2
+
+/* how the per-node child summaries are built from `k` */
+#define TA_TREE_NATURAL 0  /* child summary = mean key of the child's subtree / 2 */
+#define TA_TREE_COMPAT 1   /* reference layout: in-order Haar of block means, read in heap order */
+#define TA_TREE_NODEKEYS 2 /* `k` already holds the NL-1 heap-ordered node keys (op-level API) */
+
+typedef struct ta_problem {
+  int64_t B, L, H, D;    /* batch, query positions, heads, head dim */
+  int64_t N;             /* leaf tokens (keys/values); N = leaf_block * b^T.  Causal masks are
+                            bottom-right aligned: query t sees tokens <= t + N - L (needs L <= N) */
+  int64_t num_samples;   /* S: sampled paths per query, 1..64 */
+  int64_t branching;     /* b >= 2 */
+  int64_t leaf_block;    /* LB >= 1 */
+  int32_t tree_mode;     /* TA_TREE_* */
+  int32_t causal;        /* 0 or 1 (bottom-right aligned; L queries = L keys) */
+  int32_t dtype;         /* TA_F32 / TA_BF16 / TA_F16 */
+  int32_t reserved;
+  float scale;           /* leaf-block softmax scale */
+  float max_logit;       /* child logits are clamped to +-max_logit/2 (binary compat trees:
+                            the left/right logit to +-max_logit, _autograd.py:202) */
+  int64_t q_strides[3];  /* (batch, position, head) element strides; also dq */
+  int64_t k_strides[3];  /* (batch, token, head) of k and dk; TA_TREE_NODEKEYS: (batch, node, head) */
+  int64_t v_strides[3];  /* (batch, token, head) of v and dv */
+  int64_t o_strides[3];  /* of out */
+  int64_t g_strides[3];  /* of the incoming output gradient */
+  int64_t w_strides[3];  /* of the weights (batch, position, head); samples contiguous */
+} ta_problem;
+
+/* Library version (TA_VERSION). */
+int ta_version(void);
+
+/* Message of the last error returned on this thread ("" if none). */
+const char* ta_last_error(void);
+
+/* Sizes of the caller-allocated buffers.  `record` is written by the forward
+ * and read by the backward (the Function's saved state); the workspaces are
+ * scratch for one call each.  Replaces the reference's torch-side allocations
+ * in _autograd.py:685-700 (packed path bits + sampled indices). */
+int ta_record_bytes(const ta_problem* p, int64_t* bytes);
+int ta_forward_workspace_bytes(const ta_problem* p, int64_t* bytes);
+int ta_backward_workspace_bytes(const ta_problem* p, int64_t* bytes);
+
+/* Byte offset of a piece of the record, for callers that read the sampled
+ * paths (the reference returns them from its sampler,
+ * _autograd.py:223-257):
+ *   TA_REC_LEAVES     int32 (B, L, H, S): leaf block sampled by each path;
+ *   TA_REC_SUMMARIES  float32 (B*H, NS, D): child summaries, level-major with
+ *                     level lam (1..T) at rows sum_{m<lam} roundup32(b^m)
+ *                     (NS from TA_REC_NUM_ROWS, returned in *offset). */
+#define TA_REC_LEAVES 0
+#define TA_REC_SUMMARIES 1
+#define TA_REC_NUM_ROWS 2
+int ta_record_offset(const ta_problem* p, int which, int64_t* offset);
+
+/* Fill `out[0..n)` with the counter-RNG uniforms in (0,1) that the sampler
+ * uses when no uniform tensor is supplied (Philox4x32-10, key = seed).
+ * Replaces torch's exponential_() stream (_tree_mha.py:109,
+ * sample_non_causal_paths.cu:31-52) with a reproducible one. */
+int ta_fill_uniforms(uint64_t seed, int64_t n, float* out, void* stream);
+
+/* Per-level key summaries into the record.  Replaces haar_internal_node_keys
+ * (_treeattn_common.py:54-86) and the key re-layout in _tree_mha.py:359-365. */
+int ta_pool(const ta_problem* p, const void* k, void* record, void* stream);
+
+/* Path sampling for every (batch, position, head): one wavefront per query
+ * walks root->leaf over MFMA child-logit tiles with Gumbel-max decisions
+ * drawn from `uniforms` (B,L,H,S,T,b float32, contiguous) or, when it is
+ * NULL, from the counter RNG with `seed`.  Writes `weights` (softmax over
+ * samples, float32) and the sampled leaves into the record.  Needs ta_pool
+ * first.  Replaces sample_non_causal_paths_forward (treeattn_cuda.cpp:116;
+ * kernel sample_non_causal_paths.cu:54-241) and the softmax at
+ * _autograd.py:692,495-498. */
+int ta_sample(const ta_problem* p, const void* q, const float* uniforms, uint64_t seed,
+              float* weights, void* record, void* stream);
+
+/* Leaf-block attention and sample combine: out = sum_s w_s softmax(q K_blk^T) V_blk.
+ * Buckets (query, leaf) pairs per leaf block, then MFMA tiles per block.
+ * Needs ta_sample first.  Replaces weighted_value_sum_forward
+ * (treeattn_cuda.cpp:91; weighted_value_sum.cu:8-47). */
+int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const void* v,
+                    void* out, void* record, void* workspace, void* stream);
+
+/* Whole forward: ta_pool + ta_sample + ta_leaf_forward.  Replaces
+ * _StochasticNonCausalTreeAttention.forward (_autograd.py:645-704). */
+int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
+               const float* uniforms, uint64_t seed, void* out, float* weights,
+               void* record, void* workspace, void* stream);
+
+/* Whole backward from the forward's record: deterministic and atomic-free
+ * dq, dk, dv (each fully overwritten).  Replaces
+ * _StochasticNonCausalTreeAttention.backward (_autograd.py:706-860) with its
+ * kernels prepare_non_causal_backward (treeattn_cuda.cpp:176),
+ * scatter_weighted_grad_v_forward (:290),
+ * accumulate_qk_non_causal_all_depths_prepared_inplace (:211) and the
+ * per-depth fallbacks (:321,:367), plus the autograd of the Haar keys. */
+int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v,
+                const void* grad_out, const float* weights, const void* record,
+                void* dq, void* dk, void* dv, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREEATTN_AMD_H */

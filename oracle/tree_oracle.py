@@ -380,6 +380,7 @@ def tree_sample(
     U: np.ndarray,
     causal: bool,
     max_logit: float = 1e3,
+    N: int | None = None,
 ):
     """Per-query root-to-leaf sampling (generalizes ``_tree_mha.py:78-122``).
 
@@ -390,11 +391,14 @@ def tree_sample(
     path), and moves to ``argmax_j(logp'_j + g_j)`` (first maximum wins, as
     ``torch.argmax`` does).  Returns leaf block ids (B,L,H,S), accumulated
     log-probs (B,L,H,S) and the per-decision margins (B,L,H,S,T) between the
-    best and second-best perturbed score, for parity gating.
+    best and second-best perturbed score, for parity gating.  ``N`` (leaf
+    tokens, default ``L``) sets the causal alignment: query ``t`` sees tokens
+    ``<= t + N - L``.
     """
     B, L, H, D = q.shape
+    N = L if N is None else N
     b = branching
-    nl = L // leaf_block
+    nl = N // leaf_block
     T = tree_depth(nl, b)
     off = level_offsets(b, T)
     S = U.shape[3]
@@ -410,7 +414,7 @@ def tree_sample(
             node = np.zeros((L, S), dtype=np.int64)
             acc = np.zeros((L, S))
             if causal and T > 0:
-                blk_t = np.arange(L) // leaf_block
+                blk_t = (np.arange(L) + N - L) // leaf_block
                 digits = np.stack([(blk_t // b ** (T - 1 - d)) % b for d in range(T)], axis=-1)
                 bnode = np.stack([blk_t // b ** (T - d) for d in range(T)], axis=-1)  # (L,T)
                 cols_b = np.asarray(off[1:T + 1])[None, :, None] + b * bnode[:, :, None] + jj  # (L,T,b)
@@ -439,6 +443,35 @@ def tree_sample(
     return idx, lp, margins
 
 
+def path_logprobs(q, C, branching, num_leaf_blocks, idx, max_logit=1e3):
+    """Uncorrected ``log P(leaf)`` of given sampled leaf blocks (B,L,H,S).
+
+    In causal mode the sampler's accumulated log-probs differ from these by
+    the per-query constant ``-log A_root``, which leaves ``softmax_s``
+    (the weights) unchanged.
+    """
+    b = branching
+    T = tree_depth(num_leaf_blocks, b)
+    off = level_offsets(b, T)
+    B, L, H, D = q.shape
+    S = idx.shape[-1]
+    half = max_logit / 2
+    jj = np.arange(b)
+    lp = np.zeros((B, L, H, S))
+    for bb in range(B):
+        for h in range(H):
+            X = np.clip(q[bb, :, h].astype(np.float64) @ C[bb, h].T, -half, half)
+            leaf = idx[bb, :, h]
+            for d in range(T):
+                node = leaf // b ** (T - d)
+                js = (leaf // b ** (T - 1 - d)) % b
+                cols = off[d + 1] + b * node[..., None] + jj
+                x = np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+                logp = x - _lse(x)[..., None]
+                lp[bb, :, h] += np.take_along_axis(logp, js[..., None], axis=-1)[..., 0]
+    return lp
+
+
 def sample_weights(lp: np.ndarray) -> np.ndarray:
     """``softmax`` over samples (``_tree_mha.py:396-399``)."""
     m = lp.max(axis=-1, keepdims=True)
@@ -446,29 +479,42 @@ def sample_weights(lp: np.ndarray) -> np.ndarray:
     return e / e.sum(axis=-1, keepdims=True)
 
 
+def _leaf_gather(x64, idx_s, leaf_block):
+    """``x[b, idx*LB + j, h]`` for one sample: (B,L,H) ids -> (B,L,H,LB,D)."""
+    B, _, H, _ = x64.shape
+    tok = idx_s[..., None] * leaf_block + np.arange(leaf_block)  # (B,L,H,LB)
+    bi = np.arange(B)[:, None, None, None]
+    hi = np.arange(H)[None, None, :, None]
+    return x64[bi, tok, hi], tok
+
+
 def leaf_attention(q, k, v, idx, leaf_block, causal, scale):
     """Per (query, sample): ``softmax(scale q.K_blk^T [mask]) V_blk``.
 
     Returns ``o_s`` (B,L,H,S,D) and the probabilities (B,L,H,S,LB).  At
     ``leaf_block=1`` this is ``v[idx]``, the reference's value gather
-    (``_tree_mha.py:405``).
+    (``_tree_mha.py:405``).  Causal: query ``t`` sees tokens
+    ``<= t + N - L`` (bottom-right aligned).
     """
     B, L, H, D = q.shape
+    N = v.shape[1]
     S = idx.shape[-1]
-    LB = leaf_block
-    tok = idx[..., None] * LB + np.arange(LB)  # (B,L,H,S,LB)
-    bi = np.arange(B)[:, None, None, None, None]
-    hi = np.arange(H)[None, None, :, None, None]
-    Kg = k.astype(np.float64)[bi, tok, hi]  # (B,L,H,S,LB,D)
-    Vg = v.astype(np.float64)[bi, tok, hi]
-    z = scale * np.einsum("blhd,blhsjd->blhsj", q.astype(np.float64), Kg)
-    if causal:
-        t = np.arange(L)[None, :, None, None, None]
-        z = np.where(tok > t, -np.inf, z)
-    z = z - z.max(axis=-1, keepdims=True)
-    a = np.exp(z)
-    a = a / a.sum(axis=-1, keepdims=True)
-    return np.einsum("blhsj,blhsjd->blhsd", a, Vg), a
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    o = np.zeros((B, L, H, S, D))
+    a_all = np.zeros((B, L, H, S, leaf_block))
+    t = np.arange(L)[None, :, None, None] + (N - L)
+    for s in range(S):
+        Kg, tok = _leaf_gather(k64, idx[..., s], leaf_block)
+        Vg, _ = _leaf_gather(v64, idx[..., s], leaf_block)
+        z = scale * np.einsum("blhd,blhjd->blhj", q64, Kg)
+        if causal:
+            z = np.where(tok > t, -np.inf, z)
+        z = z - z.max(axis=-1, keepdims=True)
+        a = np.exp(z)
+        a = a / a.sum(axis=-1, keepdims=True)
+        a_all[..., s, :] = a
+        o[..., s, :] = np.einsum("blhj,blhjd->blhd", a, Vg)
+    return o, a_all
 
 
 def tree_forward(q, k, v, C, branching, leaf_block, U, causal, scale=None, max_logit=1e3):
@@ -480,7 +526,7 @@ def tree_forward(q, k, v, C, branching, leaf_block, U, causal, scale=None, max_l
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    idx, lp, margins = tree_sample(q, C, branching, leaf_block, U, causal, max_logit)
+    idx, lp, margins = tree_sample(q, C, branching, leaf_block, U, causal, max_logit, N=v.shape[1])
     w = sample_weights(lp)
     o_s, _ = leaf_attention(q, k, v, idx, leaf_block, causal, scale)
     out = np.einsum("blhs,blhsd->blhd", w, o_s)
@@ -505,7 +551,7 @@ def tree_backward(q, k, v, C, branching, leaf_block, idx, w, dout, causal, scale
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     b = branching
-    nl = L // leaf_block
+    nl = v.shape[1] // leaf_block
     T = tree_depth(nl, b)
     off = level_offsets(b, T)
     S = idx.shape[-1]
@@ -515,22 +561,23 @@ def tree_backward(q, k, v, C, branching, leaf_block, idx, w, dout, causal, scale
     delta = np.einsum("blhd,blhsd->blhs", g64, o_s)
     dlp = w * (delta - (w * delta).sum(axis=-1, keepdims=True))
 
-    tok = idx[..., None] * LB + np.arange(LB)
-    bi = np.arange(B)[:, None, None, None, None]
-    hi = np.arange(H)[None, None, :, None, None]
-    Kg = k64[bi, tok, hi]
-    Vg = v64[bi, tok, hi]
-    dP = w[..., None] * np.einsum("blhd,blhsjd->blhsj", g64, Vg)
-    dz = a * (dP - (w * delta)[..., None])
-    dq = scale * np.einsum("blhsj,blhsjd->blhd", dz, Kg)
-    dk = np.zeros((B, L, H, D))
-    dv = np.zeros((B, L, H, D))
-    dKc = scale * dz[..., None] * q64[:, :, :, None, None, :]  # (B,L,H,S,LB,D)
-    dVc = (a * w[..., None])[..., None] * g64[:, :, :, None, None, :]
-    bb = np.broadcast_to(np.arange(B)[:, None, None, None, None], tok.shape)
-    hh = np.broadcast_to(np.arange(H)[None, None, :, None, None], tok.shape)
-    np.add.at(dk, (bb, tok, hh), dKc)
-    np.add.at(dv, (bb, tok, hh), dVc)
+    N = v.shape[1]
+    dq = np.zeros((B, L, H, D))
+    dk = np.zeros((B, N, H, D))
+    dv = np.zeros((B, N, H, D))
+    for s_ in range(S):
+        Kg, tok = _leaf_gather(k64, idx[..., s_], LB)
+        Vg, _ = _leaf_gather(v64, idx[..., s_], LB)
+        ws = w[..., s_]
+        dP = ws[..., None] * np.einsum("blhd,blhjd->blhj", g64, Vg)
+        dz = a[..., s_, :] * (dP - (ws * delta[..., s_])[..., None])
+        dq += scale * np.einsum("blhj,blhjd->blhd", dz, Kg)
+        dKc = scale * dz[..., None] * q64[:, :, :, None, :]
+        dVc = (a[..., s_, :] * ws[..., None])[..., None] * g64[:, :, :, None, :]
+        bb = np.broadcast_to(np.arange(B)[:, None, None, None], tok.shape)
+        hh = np.broadcast_to(np.arange(H)[None, None, :, None], tok.shape)
+        np.add.at(dk, (bb, tok, hh), dKc)
+        np.add.at(dv, (bb, tok, hh), dVc)
 
     half = max_logit / 2
     dC = np.zeros(C.shape)
@@ -579,6 +626,6 @@ def attention_fwd_bwd(q, k, v, dout, branching, leaf_block, U, causal, tree_mode
     if dout is not None:
         dq, dC, dk_leaf, dv = tree_backward(q, k, v, C, branching, leaf_block, idx, w, dout, causal,
                                             scale, max_logit)
-        dk = dk_leaf + pool_adjoint(dC, L, branching, leaf_block, tree_mode)
+        dk = dk_leaf + pool_adjoint(dC, k.shape[1], branching, leaf_block, tree_mode)
         res.update(dq=dq, dk=dk, dv=dv, dC=dC)
     return res

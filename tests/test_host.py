@@ -1,0 +1,126 @@
+"""CPU tests of the host side: the C-ABI library loads, exports what the header
+declares, sizes and validates problems (no GPU compute), and the Python
+interfaces parse their configuration like the reference adapters."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import treeattention_amd as ta
+from treeattention_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions() -> list[str]:
+    src = open(os.path.join(ROOT, "include", "treeattn_amd.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"\b(ta_[a-z_]+)\s*\(", src)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert len(names) >= 11
+    assert set(names) == set(_lib.EXPORTS)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.ta_version() == 1
+
+
+def _problem(**kw):
+    p = _lib.Problem()
+    d = dict(B=2, L=16384, H=16, D=128, N=16384, num_samples=16, branching=4, leaf_block=64,
+             tree_mode=_lib.TA_TREE_NATURAL, causal=1, dtype=_lib.TA_BF16, scale=0.088, max_logit=1e3)
+    d.update(kw)
+    for k_, v_ in d.items():
+        setattr(p, k_, v_)
+    st = (d["L"] * d["H"] * d["D"], d["H"] * d["D"], d["D"])
+    for a in ("q_strides", "k_strides", "v_strides", "o_strides", "g_strides", "w_strides"):
+        getattr(p, a)[:] = st
+    return p
+
+
+def test_struct_layout_and_sizes():
+    assert ctypes.sizeof(_lib.Problem) == 232
+    rec, fws, bws = _lib.byte_sizes(_problem())
+    BLHS = 2 * 16384 * 16 * 16
+    assert fws >= BLHS * 128 * 2  # one bf16 partial row per (query, sample)
+    assert rec >= 4 * BLHS * 4  # leaves, slots, weights, order
+    ns = _lib.record_offset(_problem(), _lib.TA_REC_NUM_ROWS)
+    assert ns == 32 + 32 + 64 + 256  # levels 4, 16, 64, 256 padded to 32 rows
+
+
+@pytest.mark.parametrize("kw,exc", [
+    (dict(D=80), NotImplementedError),
+    (dict(num_samples=65), NotImplementedError),
+    (dict(leaf_block=256), NotImplementedError),
+    (dict(N=16384 + 64, L=16384 + 64), ValueError),  # not leaf_block * b^T
+    (dict(branching=3), ValueError),
+    (dict(tree_mode=_lib.TA_TREE_COMPAT), ValueError),  # compat is binary
+    (dict(causal=1, L=20000), ValueError),  # causal needs L <= N
+    (dict(dtype=7), ValueError),
+])
+def test_validation_errors(kw, exc):
+    with pytest.raises(exc):
+        _lib.byte_sizes(_problem(**kw))
+    assert _lib.load().ta_last_error()
+
+
+def test_resolve_num_samples(monkeypatch):
+    monkeypatch.delenv("TREEATTN_NUM_SAMPLES", raising=False)
+    assert ta.resolve_num_samples() is None
+    monkeypatch.setenv("TREEATTN_NUM_SAMPLES", "0")
+    assert ta.resolve_num_samples() is None
+    monkeypatch.setenv("TREEATTN_NUM_SAMPLES", " 16 ")
+    assert ta.resolve_num_samples() == 16
+    monkeypatch.setenv("TREEATTN_NUM_SAMPLES", "x")
+    with pytest.raises(ValueError):
+        ta.resolve_num_samples()
+    monkeypatch.setenv("TREEATTN_NUM_SAMPLES", "-2")
+    with pytest.raises(ValueError):
+        ta.resolve_num_samples()
+
+
+def test_tree_config_defaults_are_the_reference_tree(monkeypatch):
+    for n in ("TREEATTN_BRANCHING", "TREEATTN_LEAF_BLOCK", "TREEATTN_TREE_MODE", "TREEATTN_SEED"):
+        monkeypatch.delenv(n, raising=False)
+    assert ta.resolve_tree_config() == dict(branching=2, leaf_block=1, tree_mode="compat", seed=0)
+    monkeypatch.setenv("TREEATTN_TREE_MODE", "bogus")
+    with pytest.raises(ValueError):
+        ta.resolve_tree_config()
+
+
+def test_adapter_metadata():
+    ad = ta.adapter()
+    assert ad.layout == "bshd" and ad.supports_backward and ad.supports_causal
+    assert ad.is_compatible(torch.bfloat16, 128, True) == (True, "")
+    assert not ad.is_compatible(torch.bfloat16, 80, False)[0]
+
+
+def test_attn_fn_requires_num_samples(monkeypatch):
+    monkeypatch.delenv("TREEATTN_NUM_SAMPLES", raising=False)
+    x = torch.zeros(1, 16, 1, 32)
+    with pytest.raises(ValueError):
+        ta.attn_fn(x, x, x, False, None)
+
+
+def test_op_level_rejects_deterministic_mode_and_bad_shapes():
+    x = torch.zeros(8, 1, 64)
+    with pytest.raises(NotImplementedError):
+        ta.hierarchical_attention(x, x[:7], x, num_heads=2, mode="deterministic")
+    with pytest.raises(ValueError):
+        ta.hierarchical_attention(x, x[:5], x, num_heads=2)
+    with pytest.raises(ValueError):
+        ta.hierarchical_attention(x, x[:7], x, num_heads=3)
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    x = torch.zeros(1, 64, 1, 32)
+    with pytest.raises(ValueError):
+        ta.tree_attention(x, x, x, num_samples=4)

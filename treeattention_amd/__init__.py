@@ -1,0 +1,33 @@
+"""MI355X (gfx950) stochastic tree attention: hand-written HIP kernels behind a C ABI.
+
+Entry points mirror the reference interfaces: ``hierarchical_attention``
+(treeattn-torch / treeattn-cuda op), ``StochasticTreeAttention`` (the
+autograd Function), ``attn_fn`` / ``adapter`` (attn-bench kernel contract),
+plus ``tree_attention`` for the generalized tree (branching, leaf blocks).
+"""
+
+from .api import (
+    KernelAdapter,
+    adapter,
+    attn_fn,
+    hierarchical_attention,
+    resolve_num_samples,
+    resolve_tree_config,
+    tree_attention,
+)
+from .function import StochasticTreeAttention, TreeAttentionFunction, TreeOptions, tree_backward, tree_forward
+
+__all__ = [
+    "KernelAdapter",
+    "StochasticTreeAttention",
+    "TreeAttentionFunction",
+    "TreeOptions",
+    "adapter",
+    "attn_fn",
+    "hierarchical_attention",
+    "resolve_num_samples",
+    "resolve_tree_config",
+    "tree_attention",
+    "tree_backward",
+    "tree_forward",
+]

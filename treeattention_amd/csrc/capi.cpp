@@ -1,0 +1,275 @@
+// C ABI of the tree-attention library: validation, buffer layouts, launch order.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "launch.h"
+
+namespace ta {
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return TA_OK;
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+int64_t align32(int64_t x) { return (x + 31) & ~(int64_t)31; }
+
+struct Carver {
+  int64_t at = 0;
+  int64_t take(int64_t bytes) {
+    const int64_t o = at;
+    at += align256(bytes);
+    return o;
+  }
+};
+
+bool strides_ok(const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+
+// Builds and validates the plan; returns TA_OK or an error code (message set).
+int make_plan(const ta_problem* p, Plan* P) {
+  if (!p) return fail(TA_ERR_INVALID, "problem is NULL");
+  P->p = *p;
+  const int64_t B = p->B, L = p->L, N = p->N, H = p->H, D = p->D, S = p->num_samples;
+  const int64_t b = p->branching, LB = p->leaf_block;
+  if (B < 1 || L < 1 || N < 1 || H < 1)
+    return fail(TA_ERR_INVALID, "B, L, N, H must be >= 1 (got %lld, %lld, %lld, %lld)", (long long)B, (long long)L,
+                (long long)N, (long long)H);
+  if (p->causal && L > N) return fail(TA_ERR_INVALID, "causal needs L <= N (got L=%lld, N=%lld)", (long long)L, (long long)N);
+  if (D != 32 && D != 64 && D != 96 && D != 128)
+    return fail(TA_ERR_UNSUPPORTED, "head_dim must be one of 32, 64, 96, 128 (got %lld)", (long long)D);
+  if (S < 1 || S > kMaxSamples)
+    return fail(TA_ERR_UNSUPPORTED, "num_samples must be in [1, %d] (got %lld)", kMaxSamples, (long long)S);
+  if (b < 2 || b > 64) return fail(TA_ERR_INVALID, "branching must be in [2, 64] (got %lld)", (long long)b);
+  if (LB < 1 || LB > 128) return fail(TA_ERR_UNSUPPORTED, "leaf_block must be in [1, 128] (got %lld)", (long long)LB);
+  if (N % LB) return fail(TA_ERR_INVALID, "N=%lld is not a multiple of leaf_block=%lld", (long long)N, (long long)LB);
+  if (p->dtype != TA_F32 && p->dtype != TA_BF16 && p->dtype != TA_F16)
+    return fail(TA_ERR_INVALID, "unknown dtype %d", p->dtype);
+  if (p->tree_mode != TA_TREE_NATURAL && p->tree_mode != TA_TREE_COMPAT && p->tree_mode != TA_TREE_NODEKEYS)
+    return fail(TA_ERR_INVALID, "unknown tree_mode %d", p->tree_mode);
+  if (p->tree_mode != TA_TREE_NATURAL && b != 2)
+    return fail(TA_ERR_INVALID, "compat and node-key trees are binary (branching=%lld)", (long long)b);
+  if (p->tree_mode == TA_TREE_NODEKEYS && LB != 1)
+    return fail(TA_ERR_INVALID, "node-key trees have one leaf per position (leaf_block=%lld)", (long long)LB);
+  if (p->causal != 0 && p->causal != 1) return fail(TA_ERR_INVALID, "causal must be 0 or 1");
+  if (!(p->max_logit > 0.f)) return fail(TA_ERR_INVALID, "max_logit must be > 0");
+  const int64_t NL = N / LB;
+  int T = 0;
+  int64_t pw = 1;
+  while (pw < NL) {
+    pw *= b;
+    ++T;
+    if (T > kMaxDepth) break;
+  }
+  if (pw != NL || T > kMaxDepth)
+    return fail(TA_ERR_INVALID, "N/leaf_block=%lld must be a power of branching=%lld (depth <= %d)", (long long)NL,
+                (long long)b, kMaxDepth);
+  if (L * S >= (int64_t)1 << 31) return fail(TA_ERR_UNSUPPORTED, "L*num_samples must be < 2^31");
+  if (!strides_ok(p->q_strides) || !strides_ok(p->k_strides) || !strides_ok(p->v_strides) ||
+      !strides_ok(p->o_strides) || !strides_ok(p->g_strides))
+    return fail(TA_ERR_UNSUPPORTED, "tensor strides must be multiples of 8 elements");
+
+  P->B = B; P->L = L; P->N = N; P->H = H; P->D = D; P->S = S; P->BH = B * H;
+  P->esize = p->dtype == TA_F32 ? 4 : 2;
+  Geo& G = P->geo;
+  memset(&G, 0, sizeof(G));
+  G.b = (int)b; G.T = T; G.NL = (int)NL; G.LB = (int)LB;
+  G.pw[0] = 1;
+  for (int i = 1; i <= T; ++i) G.pw[i] = G.pw[i - 1] * (int)b;
+  G.off[0] = 0;
+  G.off[1] = 0;
+  for (int lam = 1; lam <= T; ++lam) G.off[lam + 1] = G.off[lam] + (int)align32(G.pw[lam]);
+  G.NS = G.off[T + 1];
+  if ((int64_t)G.NS * D * 4 * P->BH > ((int64_t)1 << 40)) return fail(TA_ERR_UNSUPPORTED, "tree too large");
+
+  // bucketing chunks: keep the (block x chunk) count table modest
+  int qc = kQueryChunk;
+  while ((int64_t)NL * ((L + qc - 1) / qc) > ((int64_t)1 << 22) && qc < L) qc *= 2;
+  P->qc = qc;
+  P->nchunk = (int)((L + qc - 1) / qc);
+  int ncol = 0;
+  for (int lam = 1; lam <= T; ++lam) ncol += (G.pw[lam] + kChunk - 1) / kChunk;
+  P->ncol = ncol;
+  const int qtiles = (int)((L + kQueryTile - 1) / kQueryTile);
+  int qsplit = ncol > 0 ? (int)((2048 + ncol * P->BH - 1) / (ncol * P->BH)) : 1;
+  if (qsplit < 1) qsplit = 1;
+  if (qsplit > qtiles) qsplit = qtiles;
+  P->qsplit = qsplit;
+
+  const int64_t BLHS = B * L * H * S;
+  const int64_t es = P->esize;
+  const bool half = es == 2;
+  Carver r;
+  P->rec.summaries = r.take(P->BH * G.NS * D * 4);
+  P->rec.sum_hi = r.take(half ? P->BH * G.NS * D * es : 0);
+  P->rec.sum_lo = r.take(half ? P->BH * G.NS * D * es : 0);
+  P->rec.sum_t = r.take(P->BH * G.NS * D * es);
+  P->rec.means = r.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : P->BH * NL * D * 4);
+  P->rec.leaf = r.take(BLHS * 4);
+  P->rec.slot_leaf = r.take(BLHS * 4);
+  P->rec.slot_weight = r.take(BLHS * 4);
+  P->rec.slot_count = r.take(B * L * H * 4);
+  P->rec.hist = r.take(P->BH * NL * P->nchunk * 4);
+  P->rec.block_start = r.take(P->BH * (NL + 1) * 4);
+  P->rec.order = r.take(P->BH * L * S * 4);
+  P->rec.total = r.at;
+  Carver f;
+  P->fws.partial = f.take(BLHS * D * es);
+  P->fws.total = f.at;
+  Carver w;
+  P->bws.delta = w.take(BLHS * 4);
+  P->bws.dq_part = w.take(BLHS * D * es);
+  P->bws.dlogp = w.take(BLHS * 4);
+  P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : B * N * H * D * 4);
+  P->bws.dsum_part = w.take((int64_t)qsplit * P->BH * G.NS * D * 4);
+  P->bws.dsum = w.take(P->BH * G.NS * D * 4);
+  P->bws.total = w.at;
+
+  if (leaf_fwd_smem(*P) < 0 || leaf_bwd_smem(*P) < 0)
+    return fail(TA_ERR_UNSUPPORTED, "leaf_block=%lld with head_dim=%lld in this dtype exceeds the 160 KiB LDS tile",
+                (long long)LB, (long long)D);
+  return TA_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(TA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" {
+
+int ta_version(void) { return TA_VERSION; }
+
+const char* ta_last_error(void) { return g_err.c_str(); }
+
+int ta_record_bytes(const ta_problem* p, int64_t* bytes) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
+  *bytes = P.rec.total;
+  return ok();
+}
+
+int ta_forward_workspace_bytes(const ta_problem* p, int64_t* bytes) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
+  *bytes = P.fws.total;
+  return ok();
+}
+
+int ta_backward_workspace_bytes(const ta_problem* p, int64_t* bytes) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
+  *bytes = P.bws.total;
+  return ok();
+}
+
+int ta_record_offset(const ta_problem* p, int which, int64_t* offset) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!offset) return fail(TA_ERR_INVALID, "offset is NULL");
+  switch (which) {
+    case TA_REC_LEAVES: *offset = P.rec.leaf; break;
+    case TA_REC_SUMMARIES: *offset = P.rec.summaries; break;
+    case TA_REC_NUM_ROWS: *offset = P.geo.NS; break;
+    default: return fail(TA_ERR_INVALID, "unknown record piece %d", which);
+  }
+  return ok();
+}
+
+int ta_fill_uniforms(uint64_t seed, int64_t n, float* out, void* stream) {
+  if (n < 0 || (n > 0 && !out)) return fail(TA_ERR_INVALID, "bad uniform buffer");
+  return launch_status(launch_fill_uniforms(seed, n, out, (hipStream_t)stream), "fill_uniforms");
+}
+
+int ta_pool(const ta_problem* p, const void* k, void* record, void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!k || !record || !aligned16(k) || !aligned16(record)) return fail(TA_ERR_INVALID, "k/record must be 16-byte aligned device pointers");
+  return launch_status(launch_pool(P, k, (char*)record, (hipStream_t)stream), "pool");
+}
+
+int ta_sample(const ta_problem* p, const void* q, const float* uniforms, uint64_t seed, float* weights, void* record,
+              void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!q || !weights || !record || !aligned16(q) || !aligned16(record))
+    return fail(TA_ERR_INVALID, "q/weights/record must be device pointers (q, record 16-byte aligned)");
+  return launch_status(launch_sample(P, q, uniforms, seed, weights, (char*)record, (hipStream_t)stream), "sample");
+}
+
+int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const void* v, void* out, void* record,
+                    void* workspace, void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
+  if (!q || !v || !out || !record || !workspace || (need_k && !k) || !aligned16(q) || !aligned16(v) ||
+      !aligned16(out) || !aligned16(record) || !aligned16(workspace) || (need_k && !aligned16(k)))
+    return fail(TA_ERR_INVALID, "q/k/v/out/record/workspace must be 16-byte aligned device pointers");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = launch_bucket(P, (char*)record, st);
+  if (e != hipSuccess) return launch_status(e, "bucket");
+  return launch_status(launch_leaf_fwd(P, q, k, v, out, (char*)record, (char*)workspace, st), "leaf_forward");
+}
+
+int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v, const float* uniforms, uint64_t seed,
+               void* out, float* weights, void* record, void* workspace, void* stream) {
+  int rc = ta_pool(p, k, record, stream);
+  if (rc) return rc;
+  rc = ta_sample(p, q, uniforms, seed, weights, record, stream);
+  if (rc) return rc;
+  return ta_leaf_forward(p, q, k, v, out, record, workspace, stream);
+}
+
+int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
+                const float* weights, const void* record, void* dq, void* dk, void* dv, void* workspace,
+                void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
+  if (!q || !v || !grad_out || !weights || !record || !dq || !dk || !dv || !workspace || (need_k && !k))
+    return fail(TA_ERR_INVALID, "NULL device pointer");
+  const void* al[] = {q, v, grad_out, record, dq, dk, dv, workspace};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = launch_leaf_bwd(P, q, k, v, grad_out, (const char*)record, dv, (char*)workspace, st);
+  if (e != hipSuccess) return launch_status(e, "leaf_backward");
+  return launch_status(launch_tree_bwd(P, q, weights, (const char*)record, dq, dk, (char*)workspace, st),
+                       "tree_backward");
+}
+
+}  // extern "C"

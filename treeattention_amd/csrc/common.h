@@ -1,0 +1,256 @@
+// Shared device/host definitions for the gfx950 tree-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "treeattn_amd.h"
+
+namespace ta {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 covers NL <= 2^24
+constexpr int kMaxSamples = 64;   // one wavefront lane per sample
+constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
+constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
+
+// Tree geometry.  Child summaries are stored level-major: level lam (1..T)
+// holds b^lam rows starting at off[lam], padded with zero rows to a multiple
+// of 32 so every MFMA tile and 16-byte load of a level stays inside it;
+// off[T+1] = NS.  Node i at depth d (0 <= i < b^d) has children rows
+// off[d+1] + b*i + j.
+struct Geo {
+  int b, T, NL, LB, NS;
+  int off[kMaxDepth + 2];
+  int pw[kMaxDepth + 1];  // pw[i] = b^i
+};
+
+// ---------------------------------------------------------------- values ---
+
+__device__ __forceinline__ float tof(float x) { return x; }
+__device__ __forceinline__ float tof(bf16 x) { return (float)x; }
+__device__ __forceinline__ float tof(f16 x) { return (float)x; }
+
+template <typename E> __device__ __forceinline__ E fromf(float x) { return (E)x; }
+
+// ------------------------------------------------------------------ MFMA ---
+// v_mfma_f32_16x16x32_{bf16,f16} / v_mfma_f32_16x16x4_f32.  Lane l supplies
+// A[row = l%16][k = KPL*(l/16) + i] and B[k = KPL*(l/16) + i][col = l%16];
+// the accumulator lane holds D[row = 4*(l/16) + r][col = l%16], r < 4.
+
+template <typename E> struct Mfma;
+
+template <> struct Mfma<bf16> {
+  static constexpr int K = 32, KPL = 8;
+  typedef bf16x8 frag;
+  __device__ static __forceinline__ f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<f16> {
+  static constexpr int K = 32, KPL = 8;
+  typedef f16x8 frag;
+  __device__ static __forceinline__ f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int K = 4, KPL = 1;
+  typedef float frag;
+  __device__ static __forceinline__ f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// KPL contiguous elements (16-byte aligned for 16-bit types).
+__device__ __forceinline__ bf16x8 ld_frag(const bf16* p) { return *(const bf16x8*)p; }
+__device__ __forceinline__ f16x8 ld_frag(const f16* p) { return *(const f16x8*)p; }
+__device__ __forceinline__ float ld_frag(const float* p) { return *p; }
+
+// KPL elements at stride s.
+__device__ __forceinline__ bf16x8 ld_frag_strided(const bf16* p, int s) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = p[i * s];
+  return r;
+}
+__device__ __forceinline__ f16x8 ld_frag_strided(const f16* p, int s) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = p[i * s];
+  return r;
+}
+__device__ __forceinline__ float ld_frag_strided(const float* p, int) { return *p; }
+
+// KPL float values converted to the MFMA element type.
+template <typename E> __device__ __forceinline__ typename Mfma<E>::frag cvt_frag(const float* p, int s);
+template <> __device__ __forceinline__ bf16x8 cvt_frag<bf16>(const float* p, int s) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (bf16)p[i * s];
+  return r;
+}
+template <> __device__ __forceinline__ f16x8 cvt_frag<f16>(const float* p, int s) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (f16)p[i * s];
+  return r;
+}
+template <> __device__ __forceinline__ float cvt_frag<float>(const float* p, int) { return *p; }
+
+// The accumulator of a (keys x queries) product used directly as the k-operand
+// of a product that reduces over keys.  Lane (g = l/16) holds keys 4g+r of
+// each 16-row tile, so k-step ks of a 16-bit MFMA takes tiles 2ks and 2ks+1:
+// slot i < 4 -> key 32ks + 4g + i, slot i >= 4 -> key 32ks + 16 + 4g + (i-4);
+// an f32 MFMA step ks takes key 16(ks/4) + 4g + ks%4.  perm_key() gives that
+// key so the other operand can be read in the same order.
+template <typename E> __device__ __forceinline__ int perm_key(int ks, int g, int i);
+template <> __device__ __forceinline__ int perm_key<bf16>(int ks, int g, int i) {
+  return 32 * ks + 16 * (i >> 2) + 4 * g + (i & 3);
+}
+template <> __device__ __forceinline__ int perm_key<f16>(int ks, int g, int i) {
+  return 32 * ks + 16 * (i >> 2) + 4 * g + (i & 3);
+}
+template <> __device__ __forceinline__ int perm_key<float>(int ks, int g, int) {
+  return 16 * (ks >> 2) + 4 * g + (ks & 3);
+}
+
+// Operand row whose keys are contiguous, read in perm_key order.
+__device__ __forceinline__ bf16x8 ld_frag_perm(const bf16* row, int ks, int g) {
+  bf16x4 a = *(const bf16x4*)(row + 32 * ks + 4 * g);
+  bf16x4 b = *(const bf16x4*)(row + 32 * ks + 16 + 4 * g);
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { r[i] = a[i]; r[i + 4] = b[i]; }
+  return r;
+}
+__device__ __forceinline__ f16x8 ld_frag_perm(const f16* row, int ks, int g) {
+  f16x4 a = *(const f16x4*)(row + 32 * ks + 4 * g);
+  f16x4 b = *(const f16x4*)(row + 32 * ks + 16 + 4 * g);
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { r[i] = a[i]; r[i + 4] = b[i]; }
+  return r;
+}
+__device__ __forceinline__ float ld_frag_perm(const float* row, int ks, int g) {
+  return row[16 * (ks >> 2) + 4 * g + (ks & 3)];
+}
+// Same order, keys strided by `s` elements.
+template <typename E> __device__ __forceinline__ typename Mfma<E>::frag ld_frag_perm_strided(const E* base, int s, int ks, int g) {
+  typename Mfma<E>::frag r;
+  if constexpr (Mfma<E>::KPL == 1) {
+    r = base[perm_key<E>(ks, g, 0) * s];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = base[perm_key<E>(ks, g, i) * s];
+  }
+  return r;
+}
+
+// Accumulator tiles as the k-operand (keys), converted to E.
+template <typename E, int NT>
+__device__ __forceinline__ typename Mfma<E>::frag acc_operand(const f32x4 (&acc)[NT], int ks) {
+  typename Mfma<E>::frag r;
+  if constexpr (Mfma<E>::KPL == 1) {
+    r = acc[ks >> 2][ks & 3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[i] = (E)acc[2 * ks][i];
+      r[i + 4] = (E)acc[2 * ks + 1][i];
+    }
+  }
+  return r;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// ------------------------------------------------------------ reductions ---
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// -------------------------------------------------------------- counter RNG ---
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).  Uniform i of a tensor is
+// word i%4 of philox(ctr = (lo(i/4), hi(i/4), 0, 0), key = seed), mapped to
+// ((x >> 8) + 0.5) * 2^-24 in (0,1).
+
+struct Philox4 { uint32_t w[4]; };
+
+__device__ __host__ inline Philox4 philox4x32_10(uint64_t ctr, uint64_t seed) {
+  uint32_t c0 = (uint32_t)ctr, c1 = (uint32_t)(ctr >> 32), c2 = 0, c3 = 0;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+  }
+  Philox4 o;
+  o.w[0] = c0; o.w[1] = c1; o.w[2] = c2; o.w[3] = c3;
+  return o;
+}
+
+__device__ __host__ inline float word_to_uniform(uint32_t x) {
+  return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------- record layout ---
+// Byte offsets of the saved record and the workspaces inside the caller's
+// buffers (256-byte aligned pieces).
+
+struct RecordLayout {
+  int64_t summaries;   // float (BH, NS, D)
+  int64_t sum_hi;      // E (BH, NS, D): E-rounded summaries (float inputs: unused)
+  int64_t sum_lo;      // E (BH, NS, D): summaries - hi
+  int64_t sum_t;       // E (BH, D, NS): hi, transposed (float inputs: float)
+  int64_t means;       // float (BH, NL, D) leaf-block means
+  int64_t leaf;        // int (B, L, H, S): leaf block of each sample
+  int64_t slot_leaf;   // int (B, L, H, S): distinct leaf blocks, ascending
+  int64_t slot_weight; // float (B, L, H, S): summed weight per distinct leaf block
+  int64_t slot_count;  // int (B, L, H)
+  int64_t hist;        // int (BH, NL, nchunk): pair counts, then scanned offsets
+  int64_t block_start; // int (BH, NL + 1)
+  int64_t order;       // int (BH, L*S): (l*S + u) grouped by leaf block
+  int64_t total;
+};
+
+struct FwdWorkspaceLayout {
+  int64_t partial;  // E (B, L, H, S, D): w * o per distinct leaf block
+  int64_t total;
+};
+
+struct BwdWorkspaceLayout {
+  int64_t delta;     // float (B, L, H, S): dout . o per distinct leaf block
+  int64_t dq_part;   // E (B, L, H, S, D): leaf dq per distinct leaf block
+  int64_t dlogp;     // float (B, L, H, S): gradient of each sample's log-prob
+  int64_t dk_leaf;   // float (B, N, H, D)
+  int64_t dsum_part; // float (qsplit, BH, NS, D)
+  int64_t dsum;      // float (BH, NS, D)
+  int64_t total;
+};
+
+constexpr int kQueryChunk = 256; // queries per bucketing chunk (one wavefront each)
+
+}  // namespace ta

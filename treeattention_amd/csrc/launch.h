@@ -1,0 +1,48 @@
+// Host-side plan and kernel launchers shared by the C ABI (capi.cpp).
+#pragma once
+
+#include "common.h"
+
+namespace ta {
+
+// Everything derived from a ta_problem that the launchers need.
+struct Plan {
+  ta_problem p;
+  Geo geo;
+  int64_t B, L, N, H, D, S, BH;  // L queries, N leaf tokens
+  int esize;        // bytes per element of q/k/v
+  int qc;           // queries per bucketing chunk
+  int nchunk;       // bucketing chunks per (batch, head)
+  int ncol;         // child-summary chunks of kChunk columns over all levels
+  int qsplit;       // query splits of the summary-gradient kernel
+  RecordLayout rec;
+  FwdWorkspaceLayout fws;
+  BwdWorkspaceLayout bws;
+};
+
+// pool.hip
+hipError_t launch_pool(const Plan& P, const void* k, char* rec, hipStream_t st);
+hipError_t launch_fill_uniforms(uint64_t seed, int64_t n, float* out, hipStream_t st);
+// sample.hip
+hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
+                         float* weights, char* rec, hipStream_t st);
+// bucket.hip
+hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st);
+// leaf_fwd.hip
+hipError_t launch_leaf_fwd(const Plan& P, const void* q, const void* k, const void* v,
+                           void* out, char* rec, char* ws, hipStream_t st);
+// leaf_bwd.hip
+hipError_t launch_leaf_bwd(const Plan& P, const void* q, const void* k, const void* v,
+                           const void* g, const char* rec, void* dv, char* ws, hipStream_t st);
+// tree_bwd.hip
+hipError_t launch_tree_bwd(const Plan& P, const void* q, const float* weights, const char* rec,
+                           void* dq, void* dk, char* ws, hipStream_t st);
+
+// Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
+// variant fits in 160 KiB.
+int leaf_fwd_smem(const Plan& P);
+int leaf_bwd_smem(const Plan& P);
+
+inline int padded_keys(int LB) { return LB <= 32 ? 32 : (LB <= 64 ? 64 : 128); }
+
+}  // namespace ta

@@ -1,0 +1,304 @@
+// K4a: leaf-block backward.
+//
+// One workgroup per (leaf block, batch*head) walks every (query, leaf block)
+// pair of its bucket in 64-pair tiles and keeps dV_blk and dK_blk in
+// registers for the whole bucket, so each leaf token's gradient is produced
+// by exactly one workgroup in a fixed order: no atomics (the reference
+// scatters with gpuAtomicAdd, scatter_weighted_grad_v.cu:49-52 and
+// accumulate_qk_non_causal.cu:71-74).  Per tile (g = output gradient row of
+// the pair's query, w = the pair's summed sample weight):
+//   S^T = K Q^T, P = softmax over keys             (recomputed)
+//   dP^T = V g^T, delta = sum_keys P dP = g . o     (-> the tree backward)
+//   dz = w P (dP - delta)
+//   dq_pair^T = scale K^T dz^T                     (-> per-pair slot, summed in tree_bwd)
+//   dV += (w P)^T g,  dK += scale dz^T Q            (P^T and dz^T staged in LDS)
+#include "launch.h"
+
+namespace ta {
+
+struct LeafBwdArgs {
+  int L, N, H, S, NL, LB, causal;
+  float scale, scale_log2;
+  const void *q, *k, *v, *g;
+  int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh, gsb, gsl, gsh;
+  const int* order;
+  const int* block_start;
+  const float* slot_weight;
+  float* delta;     // (B,L,H,S)
+  void* dq_part;    // E (B,L,H,S,D)
+  void* dv;         // E, v strides
+  float* dk_leaf;   // (B,L,H,D) or null
+};
+
+template <typename E>
+__device__ __forceinline__ void mov8(E* o, const E* p) {
+  if constexpr (sizeof(E) == 2) {
+    *(uint4*)o = *(const uint4*)p;
+  } else {
+    *(float4*)o = *(const float4*)p;
+    *(float4*)(o + 4) = *(const float4*)(p + 4);
+  }
+}
+template <typename E>
+__device__ __forceinline__ void zero8e(E* o) {
+  if constexpr (sizeof(E) == 2) {
+    *(uint4*)o = make_uint4(0, 0, 0, 0);
+  } else {
+    *(float4*)o = make_float4(0, 0, 0, 0);
+    *(float4*)(o + 4) = make_float4(0, 0, 0, 0);
+  }
+}
+
+template <typename E, int D, int LBP>
+__global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
+  using M = Mfma<E>;
+  constexpr int QT = 64;
+  constexpr int NT = (LBP / 16) * (D / 16) / 4;  // dV / dK tiles per wave
+  extern __shared__ __align__(16) char smem[];
+  E* Ks = (E*)smem;       // [LBP][D]
+  E* Vs = Ks + LBP * D;   // [LBP][D]
+  E* Qs = Vs + LBP * D;   // [QT][D]
+  E* Gs = Qs + QT * D;    // [QT][D]
+  E* Pt = Gs + QT * D;    // [LBP][QT]  (w P)^T
+  E* Zt = Pt + LBP * QT;  // [LBP][QT]  dz^T
+  int* ent_s = (int*)(Zt + LBP * QT);
+
+  const int beta = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
+  const int start = bs[beta], end = bs[beta + 1];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int LB = a.LB, S = a.S;
+  const int64_t LS = (int64_t)a.L * S;
+  const E* q = (const E*)a.q;
+  const E* k = (const E*)a.k;
+  const E* v = (const E*)a.v;
+  const E* go = (const E*)a.g;
+
+  for (int e = tid; e < LBP * D / 8; e += 256) {
+    const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+    const int64_t tok = (int64_t)beta * LB + key;
+    if (key < LB && k) mov8(Ks + key * D + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+    else zero8e(Ks + key * D + c);
+    if (key < LB) mov8(Vs + key * D + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+    else zero8e(Vs + key * D + c);
+  }
+
+  f32x4 dvacc[NT], dkacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) { dvacc[t] = zero4(); dkacc[t] = zero4(); }
+
+  for (int t0 = start; t0 < end; t0 += QT) {
+    __syncthreads();
+    if (tid < QT) ent_s[tid] = (t0 + tid < end) ? a.order[(int64_t)bh * LS + t0 + tid] : -1;
+    __syncthreads();
+    for (int e = tid; e < QT * D / 8; e += 256) {
+      const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
+      const int ent = ent_s[r];
+      if (ent >= 0) {
+        const int l = ent / S;
+        mov8(Qs + r * D + c, q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + c);
+        mov8(Gs + r * D + c, go + bb * a.gsb + (int64_t)l * a.gsl + h * a.gsh + c);
+      } else {
+        zero8e(Qs + r * D + c);
+        zero8e(Gs + r * D + c);
+      }
+    }
+    __syncthreads();
+
+    const int qcol = 16 * w + col;
+    const int ent = ent_s[qcol];
+    const bool valid = ent >= 0;
+    const int l = valid ? ent / S : 0, u = valid ? ent - l * S : 0;
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+
+    f32x4 sacc[LBP / 16], pacc[LBP / 16];
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt) {
+      sacc[mt] = zero4();
+      pacc[mt] = zero4();
+      const E* kp = Ks + (16 * mt + col) * D + M::KPL * g;
+      const E* vp = Vs + (16 * mt + col) * D + M::KPL * g;
+      const E* qp = Qs + qcol * D + M::KPL * g;
+      const E* gp = Gs + qcol * D + M::KPL * g;
+#pragma unroll
+      for (int ks = 0; ks < D / M::K; ++ks) {
+        sacc[mt] = M::mma(ld_frag(kp + ks * M::K), ld_frag(qp + ks * M::K), sacc[mt]);
+        pacc[mt] = M::mma(ld_frag(vp + ks * M::K), ld_frag(gp + ks * M::K), pacc[mt]);
+      }
+    }
+    const int kmax = valid ? (a.causal ? min(LB, l + (a.N - a.L) - beta * LB + 1) : LB) : 0;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
+        sacc[mt][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = (16 * mt + 4 * g + r) < kmax ? exp2f(sacc[mt][r] - mx) : 0.f;
+        sacc[mt][r] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    float delta = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sacc[mt][r] *= inv;
+        delta += sacc[mt][r] * pacc[mt][r];
+      }
+    delta += __shfl_xor(delta, 16, 64);
+    delta += __shfl_xor(delta, 32, 64);
+    const float wt = valid ? a.slot_weight[qh * S + u] : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * mt + 4 * g + r;
+        const float p = sacc[mt][r];
+        const float dz = wt * p * (pacc[mt][r] - delta);
+        pacc[mt][r] = dz;
+        Pt[key * QT + qcol] = (E)(wt * p);
+        Zt[key * QT + qcol] = (E)dz;
+      }
+    if (valid && g == 0) a.delta[qh * S + u] = delta;
+
+    E* dqp = (E*)a.dq_part + (qh * S + u) * D;
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md) {
+      f32x4 o = zero4();
+      const E* kcol = Ks + 16 * md + col;
+#pragma unroll
+      for (int ks = 0; ks < LBP / M::K; ++ks)
+        o = M::mma(ld_frag_perm_strided<E>(kcol, D, ks, g), acc_operand<E>(pacc, ks), o);
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dqp[16 * md + 4 * g + r] = (E)(o[r] * a.scale);
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = w + 4 * t;
+      const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
+      const E* pa = Pt + (16 * mk + col) * QT + M::KPL * g;
+      const E* za = Zt + (16 * mk + col) * QT + M::KPL * g;
+      const E* gb = Gs + (M::KPL * g) * D + 16 * nd + col;
+      const E* qb = Qs + (M::KPL * g) * D + 16 * nd + col;
+#pragma unroll
+      for (int ks = 0; ks < QT / M::K; ++ks) {
+        dvacc[t] = M::mma(ld_frag(pa + ks * M::K), ld_frag_strided(gb + ks * M::K * D, D), dvacc[t]);
+        dkacc[t] = M::mma(ld_frag(za + ks * M::K), ld_frag_strided(qb + ks * M::K * D, D), dkacc[t]);
+      }
+    }
+  }
+
+  E* dv = (E*)a.dv;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = w + 4 * t;
+    const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = 16 * mk + 4 * g + r;
+      if (key < LB) {
+        const int64_t tok = (int64_t)beta * LB + key;
+        const int d = 16 * nd + col;
+        dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[t][r];
+        if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[t][r] * a.scale;
+      }
+    }
+  }
+}
+
+template <typename E, int D, int LBP>
+static int bwd_smem_t() {
+  return (2 * LBP * D + 2 * 64 * D + 2 * LBP * 64) * (int)sizeof(E) + 64 * 4;
+}
+
+int leaf_bwd_smem(const Plan& P) {
+  const int LBP = padded_keys(P.geo.LB);
+  const int s = (2 * LBP * (int)P.D + 2 * 64 * (int)P.D + 2 * LBP * 64) * P.esize + 64 * 4;
+  return s <= 160 * 1024 ? s : -1;
+}
+
+template <typename E, int D, int LBP>
+static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, const void* v, const void* g,
+                                const char* rec, void* dv, char* ws, hipStream_t st) {
+  LeafBwdArgs a;
+  a.L = (int)P.L;
+  a.N = (int)P.N;
+  a.H = (int)P.H;
+  a.S = (int)P.S;
+  a.NL = P.geo.NL;
+  a.LB = P.geo.LB;
+  a.causal = P.p.causal;
+  a.scale = P.p.scale;
+  a.scale_log2 = P.p.scale * 1.4426950408889634f;
+  const bool nodekeys = P.p.tree_mode == TA_TREE_NODEKEYS;
+  a.q = q;
+  a.k = nodekeys ? nullptr : k;
+  a.v = v;
+  a.g = g;
+  a.qsb = P.p.q_strides[0]; a.qsl = P.p.q_strides[1]; a.qsh = P.p.q_strides[2];
+  a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
+  a.vsb = P.p.v_strides[0]; a.vsl = P.p.v_strides[1]; a.vsh = P.p.v_strides[2];
+  a.gsb = P.p.g_strides[0]; a.gsl = P.p.g_strides[1]; a.gsh = P.p.g_strides[2];
+  a.order = (const int*)(rec + P.rec.order);
+  a.block_start = (const int*)(rec + P.rec.block_start);
+  a.slot_weight = (const float*)(rec + P.rec.slot_weight);
+  a.delta = (float*)(ws + P.bws.delta);
+  a.dq_part = ws + P.bws.dq_part;
+  a.dv = dv;
+  a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
+  const int smem = bwd_smem_t<E, D, LBP>();
+  hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((leaf_bwd_kernel<E, D, LBP>), dim3(P.geo.NL, P.BH), dim3(256), smem, st, a);
+  return hipGetLastError();
+}
+
+template <typename E, int D>
+static hipError_t leaf_bwd_lb(const Plan& P, const void* q, const void* k, const void* v, const void* g,
+                              const char* rec, void* dv, char* ws, hipStream_t st) {
+  switch (padded_keys(P.geo.LB)) {
+    case 32: return leaf_bwd_impl<E, D, 32>(P, q, k, v, g, rec, dv, ws, st);
+    case 64: return leaf_bwd_impl<E, D, 64>(P, q, k, v, g, rec, dv, ws, st);
+    default: return leaf_bwd_impl<E, D, 128>(P, q, k, v, g, rec, dv, ws, st);
+  }
+}
+
+template <typename E>
+static hipError_t leaf_bwd_d(const Plan& P, const void* q, const void* k, const void* v, const void* g,
+                             const char* rec, void* dv, char* ws, hipStream_t st) {
+  switch (P.D) {
+    case 32: return leaf_bwd_lb<E, 32>(P, q, k, v, g, rec, dv, ws, st);
+    case 64: return leaf_bwd_lb<E, 64>(P, q, k, v, g, rec, dv, ws, st);
+    case 96: return leaf_bwd_lb<E, 96>(P, q, k, v, g, rec, dv, ws, st);
+    default: return leaf_bwd_lb<E, 128>(P, q, k, v, g, rec, dv, ws, st);
+  }
+}
+
+hipError_t launch_leaf_bwd(const Plan& P, const void* q, const void* k, const void* v, const void* g,
+                           const char* rec, void* dv, char* ws, hipStream_t st) {
+  switch (P.p.dtype) {
+    case TA_F32: return leaf_bwd_d<float>(P, q, k, v, g, rec, dv, ws, st);
+    case TA_BF16: return leaf_bwd_d<bf16>(P, q, k, v, g, rec, dv, ws, st);
+    default: return leaf_bwd_d<f16>(P, q, k, v, g, rec, dv, ws, st);
+  }
+}
+
+}  // namespace ta

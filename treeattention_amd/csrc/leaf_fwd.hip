@@ -1,0 +1,249 @@
+// K3: leaf-block attention for every sampled (query, leaf block) pair, then
+// the combine over samples.
+//
+// The reference gathers v[leaf] per sample and sums with the sample weights
+// (_tree_mha.py:401-407; weighted_value_sum.cu:8-47).  With leaf blocks of LB
+// keys each pair needs softmax(scale q K_blk^T) V_blk, so pairs are bucketed
+// per leaf block (bucket.hip) and one workgroup per (leaf block, batch*head)
+// keeps K_blk / V_blk in LDS while 64-pair tiles run through two MFMA
+// products:  S^T = K Q^T (keys x queries), then O^T = V^T P^T with P^T taken
+// straight from the S^T accumulator registers.  Each pair's w * o lands in
+// its own slot of the partial buffer; combine_kernel sums the slots of each
+// query in slot order, so the forward is deterministic without atomics.
+#include "launch.h"
+
+namespace ta {
+
+struct LeafFwdArgs {
+  int L, H, S, NL, LB, causal, coff;
+  float scale_log2;
+  const void *q, *k, *v;
+  int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh;
+  const int* order;
+  const int* block_start;
+  const float* slot_weight;
+  void* partial;
+};
+
+template <typename E>
+__device__ __forceinline__ void load8(E* o, const E* p) {
+  if constexpr (sizeof(E) == 2) {
+    *(uint4*)o = *(const uint4*)p;
+  } else {
+    *(float4*)o = *(const float4*)p;
+    *(float4*)(o + 4) = *(const float4*)(p + 4);
+  }
+}
+
+template <typename E, int D, int LBP>
+__global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
+  using M = Mfma<E>;
+  constexpr int QT = 64;
+  extern __shared__ __align__(16) char smem[];
+  E* Ks = (E*)smem;        // [LBP][D]
+  E* Vt = Ks + LBP * D;    // [D][LBP]
+  E* Qs = Vt + D * LBP;    // [QT][D]
+  int* ent_s = (int*)(Qs + QT * D);
+
+  const int beta = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
+  const int start = bs[beta], end = bs[beta + 1];
+  if (start >= end) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int LB = a.LB, S = a.S;
+  const int64_t LS = (int64_t)a.L * S;
+  const E* q = (const E*)a.q;
+  const E* k = (const E*)a.k;
+  const E* v = (const E*)a.v;
+
+  for (int e = tid; e < LBP * D / 8; e += 256) {
+    const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+    alignas(16) E kv[8];
+    alignas(16) E vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { kv[i] = (E)0.f; vv[i] = (E)0.f; }
+    if (key < LB) {
+      const int64_t tok = (int64_t)beta * LB + key;
+      if (k) load8(kv, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+      load8(vv, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+    }
+    load8(Ks + key * D + c, kv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Vt[(c + i) * LBP + key] = vv[i];
+  }
+
+  for (int t0 = start; t0 < end; t0 += QT) {
+    __syncthreads();
+    if (tid < QT) ent_s[tid] = (t0 + tid < end) ? a.order[(int64_t)bh * LS + t0 + tid] : -1;
+    __syncthreads();
+    for (int e = tid; e < QT * D / 8; e += 256) {
+      const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
+      const int ent = ent_s[r];
+      if (ent >= 0) {
+        const int l = ent / S;
+        load8(Qs + r * D + c, q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + c);
+      } else {
+        alignas(16) E z[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) z[i] = (E)0.f;
+        load8(Qs + r * D + c, z);
+      }
+    }
+    __syncthreads();
+
+    const int qcol = 16 * w + col;
+    const int ent = ent_s[qcol];
+    const bool valid = ent >= 0;
+    const int l = valid ? ent / S : 0, u = valid ? ent - l * S : 0;
+
+    f32x4 sacc[LBP / 16];
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt) {
+      sacc[mt] = zero4();
+      const E* ap = Ks + (16 * mt + col) * D + M::KPL * g;
+      const E* bp = Qs + qcol * D + M::KPL * g;
+#pragma unroll
+      for (int ks = 0; ks < D / M::K; ++ks) sacc[mt] = M::mma(ld_frag(ap + ks * M::K), ld_frag(bp + ks * M::K), sacc[mt]);
+    }
+    // keys < kmax are visible to this query
+    const int kmax = valid ? (a.causal ? min(LB, l + a.coff - beta * LB + 1) : LB) : 0;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * mt + 4 * g + r;
+        const float s = key < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
+        sacc[mt][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = (16 * mt + 4 * g + r) < kmax ? exp2f(sacc[mt][r] - mx) : 0.f;
+        sacc[mt][r] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+    const float f = (valid && sum > 0.f) ? a.slot_weight[qh * S + u] / sum : 0.f;
+    E* dst = (E*)a.partial + (qh * S + u) * D;
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md) {
+      f32x4 o = zero4();
+      const E* vrow = Vt + (16 * md + col) * LBP;
+#pragma unroll
+      for (int ks = 0; ks < LBP / M::K; ++ks) o = M::mma(ld_frag_perm(vrow, ks, g), acc_operand<E>(sacc, ks), o);
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[16 * md + 4 * g + r] = (E)(o[r] * f);
+      }
+    }
+  }
+}
+
+// out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows.
+template <typename E, int D>
+__global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
+                                                      E* __restrict__ out, int L, int H, int S, int64_t nqh,
+                                                      int64_t osb, int64_t osl, int64_t osh) {
+  constexpr int TPQ = D / 4;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t qh = gid / TPQ;
+  if (qh >= nqh) return;
+  const int part = (int)(gid - qh * TPQ);
+  const int n = slot_count[qh];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const E* p = partial + qh * S * D + 4 * part;
+  for (int u = 0; u < n; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += tof(p[(int64_t)u * D + i]);
+  const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
+  E* o = out + bb * osb + l * osl + h * osh + 4 * part;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (E)acc[i];
+}
+
+template <typename E, int D, int LBP>
+static int fwd_smem_t() {
+  return (2 * LBP * D + 64 * D) * (int)sizeof(E) + 64 * 4;
+}
+
+int leaf_fwd_smem(const Plan& P) {
+  const int LBP = padded_keys(P.geo.LB);
+  const int s = (2 * LBP * (int)P.D + 64 * (int)P.D) * P.esize + 64 * 4;
+  return s <= 160 * 1024 ? s : -1;
+}
+
+template <typename E, int D, int LBP>
+static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
+                                char* ws, hipStream_t st) {
+  LeafFwdArgs a;
+  a.L = (int)P.L;
+  a.H = (int)P.H;
+  a.S = (int)P.S;
+  a.NL = P.geo.NL;
+  a.LB = P.geo.LB;
+  a.causal = P.p.causal;
+  a.coff = (int)(P.N - P.L);
+  a.scale_log2 = P.p.scale * 1.4426950408889634f;
+  a.q = q;
+  a.k = P.p.tree_mode == TA_TREE_NODEKEYS ? nullptr : k;
+  a.v = v;
+  a.qsb = P.p.q_strides[0]; a.qsl = P.p.q_strides[1]; a.qsh = P.p.q_strides[2];
+  a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
+  a.vsb = P.p.v_strides[0]; a.vsl = P.p.v_strides[1]; a.vsh = P.p.v_strides[2];
+  a.order = (const int*)(rec + P.rec.order);
+  a.block_start = (const int*)(rec + P.rec.block_start);
+  a.slot_weight = (const float*)(rec + P.rec.slot_weight);
+  a.partial = ws + P.fws.partial;
+  const int smem = fwd_smem_t<E, D, LBP>();
+  hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(P.geo.NL, P.BH), dim3(256), smem, st, a);
+  const int64_t nqh = P.B * P.L * P.H;
+  const int64_t nthr = nqh * (D / 4);
+  hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
+                     (const E*)a.partial, (const int*)(rec + P.rec.slot_count), (E*)out, (int)P.L, (int)P.H,
+                     (int)P.S, nqh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2]);
+  return hipGetLastError();
+}
+
+template <typename E, int D>
+static hipError_t leaf_fwd_lb(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
+                              char* ws, hipStream_t st) {
+  switch (padded_keys(P.geo.LB)) {
+    case 32: return leaf_fwd_impl<E, D, 32>(P, q, k, v, out, rec, ws, st);
+    case 64: return leaf_fwd_impl<E, D, 64>(P, q, k, v, out, rec, ws, st);
+    default: return leaf_fwd_impl<E, D, 128>(P, q, k, v, out, rec, ws, st);
+  }
+}
+
+template <typename E>
+static hipError_t leaf_fwd_d(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
+                             char* ws, hipStream_t st) {
+  switch (P.D) {
+    case 32: return leaf_fwd_lb<E, 32>(P, q, k, v, out, rec, ws, st);
+    case 64: return leaf_fwd_lb<E, 64>(P, q, k, v, out, rec, ws, st);
+    case 96: return leaf_fwd_lb<E, 96>(P, q, k, v, out, rec, ws, st);
+    default: return leaf_fwd_lb<E, 128>(P, q, k, v, out, rec, ws, st);
+  }
+}
+
+hipError_t launch_leaf_fwd(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec, char* ws,
+                           hipStream_t st) {
+  switch (P.p.dtype) {
+    case TA_F32: return leaf_fwd_d<float>(P, q, k, v, out, rec, ws, st);
+    case TA_BF16: return leaf_fwd_d<bf16>(P, q, k, v, out, rec, ws, st);
+    default: return leaf_fwd_d<f16>(P, q, k, v, out, rec, ws, st);
+  }
+}
+
+}  // namespace ta

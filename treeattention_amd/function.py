@@ -1,0 +1,246 @@
+"""Autograd Function over the HIP library.
+
+``TreeAttentionFunction`` is the MI355X counterpart of treeattn-cuda's
+``_StochasticNonCausalTreeAttention`` (``_autograd.py:645-860``): the forward
+samples paths and combines the leaf outputs, saves a compact record (the
+sampled leaf blocks, their weights and the per-leaf-block bucket), and the
+backward replays nothing on the host: one call produces dq, dk, dv.  The
+sample weights are returned as a non-differentiable output, as in the
+reference (``_autograd.py:703``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.TA_F32, torch.bfloat16: _lib.TA_BF16, torch.float16: _lib.TA_F16}
+
+
+@dataclass(frozen=True)
+class TreeOptions:
+    """How the tree is built and sampled.
+
+    * ``num_samples``: paths per query (1..64).
+    * ``branching``, ``leaf_block``: ``N = leaf_block * branching**T``.
+    * ``tree_mode``: ``"compat"`` (reference key layout: in-order Haar of the
+      leaf-block means, read in heap order), ``"natural"`` (child summary =
+      half the mean key of the child's subtree) or ``"nodekeys"`` (``k`` holds
+      the heap-ordered node keys, the op-level reference API).
+    * ``causal``: bottom-right aligned mask; sampling is restricted exactly to
+      allowed leaf blocks.
+    * ``scale``: leaf-block softmax scale (``None`` -> ``1/sqrt(D)``).
+    * ``max_logit``: child logits are clamped to ``+-max_logit/2``.
+    * ``seed``: counter-RNG key for the Gumbel uniforms when no explicit
+      ``uniforms`` tensor is given.
+    * ``layout``: ``"bshd"`` (B, L, H, D) or ``"lbhd"`` (L, B, H, D).
+    """
+
+    num_samples: int
+    branching: int = 2
+    leaf_block: int = 1
+    tree_mode: str = "compat"
+    causal: bool = False
+    scale: float | None = None
+    max_logit: float = 1e3
+    seed: int = 0
+    layout: str = "bshd"
+
+
+def _bl(t: torch.Tensor, layout: str) -> tuple[int, int]:
+    """(batch, position) sizes of a 4-D tensor in ``layout``."""
+    return (t.shape[0], t.shape[1]) if layout == "bshd" else (t.shape[1], t.shape[0])
+
+
+def _strides(t: torch.Tensor, layout: str):
+    s = t.stride()
+    return (s[0], s[1], s[2]) if layout == "bshd" else (s[1], s[0], s[2])
+
+
+def _prep(t: torch.Tensor) -> torch.Tensor:
+    """Last dim contiguous, other strides multiples of 8, 16-byte aligned."""
+    if t.stride(-1) != 1 or any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def make_problem(q, k, v, opts: TreeOptions) -> _lib.Problem:
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q/k/v must share one of {list(_DTYPES)} (got {q.dtype}, {k.dtype}, {v.dtype})")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("q, k, v must be on a GPU device")
+    B, L = _bl(q, opts.layout)
+    Bv, N = _bl(v, opts.layout)
+    H, D = q.shape[2], q.shape[3]
+    if Bv != B or v.shape[2] != H or v.shape[3] != D or k.shape[2] != H or k.shape[3] != D:
+        raise ValueError(f"incompatible shapes q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    if opts.tree_mode == "nodekeys":
+        if _bl(k, opts.layout)[1] != N - 1:
+            raise ValueError(f"Key tensor length must be N-1 ({N - 1}), but got {_bl(k, opts.layout)[1]}.")
+    elif _bl(k, opts.layout)[1] != N:
+        raise ValueError(f"k and v must have the same length (got {_bl(k, opts.layout)[1]} and {N})")
+    p = _lib.Problem()
+    p.B, p.L, p.H, p.D, p.N = B, L, H, D, N
+    p.num_samples = opts.num_samples
+    p.branching = opts.branching
+    p.leaf_block = opts.leaf_block
+    p.tree_mode = _lib.TREE_MODES[opts.tree_mode]
+    p.causal = int(bool(opts.causal))
+    p.dtype = _DTYPES[q.dtype]
+    p.scale = float(opts.scale) if opts.scale is not None else 1.0 / math.sqrt(D)
+    p.max_logit = float(opts.max_logit)
+    p.q_strides[:] = _strides(q, opts.layout)
+    p.k_strides[:] = _strides(k, opts.layout)
+    p.v_strides[:] = _strides(v, opts.layout)
+    p.o_strides[:] = _strides(q, opts.layout)
+    p.g_strides[:] = _strides(q, opts.layout)
+    return p
+
+
+def _weights_like(q: torch.Tensor, S: int, layout: str) -> tuple[torch.Tensor, tuple[int, int, int]]:
+    w = torch.empty((*q.shape[:3], S), device=q.device, dtype=torch.float32)
+    return w, _strides(w, layout)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = None):
+    """Forward only: returns ``(out, weights, record)``."""
+    lib = _lib.load()
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    prob = make_problem(q, k, v, opts)
+    rec_b, fws_b, _ = _lib.byte_sizes(prob)
+    out = torch.empty_like(q)
+    prob.o_strides[:] = _strides(out, opts.layout)
+    weights, ws = _weights_like(q, opts.num_samples, opts.layout)
+    prob.w_strides[:] = ws
+    record = torch.empty(rec_b, device=q.device, dtype=torch.uint8)
+    work = torch.empty(fws_b, device=q.device, dtype=torch.uint8)
+    if uniforms is not None:
+        expect = (prob.B, prob.L, prob.H, opts.num_samples)
+        if (uniforms.dtype != torch.float32 or not uniforms.is_contiguous() or uniforms.device != q.device
+                or tuple(uniforms.shape[:4]) != expect or uniforms.dim() != 6
+                or uniforms.shape[5] != opts.branching):
+            raise ValueError(
+                f"uniforms must be a contiguous float32 (B, L, H, S, T, b) tensor on {q.device}, "
+                f"leading dims {expect}; got {tuple(uniforms.shape)} {uniforms.dtype}")
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ta_forward(ctypes.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(uniforms),
+                                  ctypes.c_uint64(opts.seed & 0xFFFFFFFFFFFFFFFF), out.data_ptr(),
+                                  weights.data_ptr(), record.data_ptr(), work.data_ptr(), _stream(q.device)))
+    return out, weights, record
+
+
+def tree_backward(q, k, v, weights, record, grad_out, opts: TreeOptions):
+    """Backward from a forward record: returns ``(dq, dk, dv)``."""
+    lib = _lib.load()
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    grad_out = _prep(grad_out)
+    prob = make_problem(q, k, v, opts)
+    prob.g_strides[:] = _strides(grad_out, opts.layout)
+    prob.w_strides[:] = _strides(weights, opts.layout)
+    _, _, bws_b = _lib.byte_sizes(prob)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    work = torch.empty(bws_b, device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ta_backward(ctypes.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                                   weights.data_ptr(), record.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                   dv.data_ptr(), work.data_ptr(), _stream(q.device)))
+    return dq, dk, dv
+
+
+class TreeAttentionFunction(torch.autograd.Function):
+    """``apply(q, k, v, opts, uniforms=None) -> (out, weights)``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, opts: TreeOptions, uniforms=None):
+        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+        ctx.save_for_backward(q, k, v, weights, record)
+        ctx.opts = opts
+        ctx.mark_non_differentiable(weights)
+        return out, weights
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_weights):
+        del grad_weights
+        q, k, v, weights, record = ctx.saved_tensors
+        dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, ctx.opts)
+        return dq, dk, dv, None, None
+
+
+class StochasticTreeAttention(torch.autograd.Function):
+    """Drop-in for treeattn-cuda's ``_StochasticNonCausalTreeAttention``.
+
+    ``apply(q (L,B,H,D), k (N-1,B,H,D) heap-ordered node keys, v (N,B,H,D),
+    num_samples, block_size, max_logit, is_causal=False, seed=0,
+    uniforms=None) -> (out (L,B,H,D), weights (L,B,H,S) float32)``, gradients
+    ``(dq, dk, dv, None, ...)`` (``_autograd.py:645-707,860``).  ``block_size``
+    (the reference's query streaming) does not change results and is
+    accepted for compatibility.  Edge cases follow ``_autograd.py:660-683``.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, num_samples, block_size=256, max_logit=1e3, is_causal=False, seed=0, uniforms=None):
+        del block_size
+        num_leaves = v.shape[0]
+        if num_samples <= 0:
+            raise ValueError(f"num_samples must be > 0, got {num_samples}")
+        ctx.num_leaves = num_leaves
+        if num_leaves <= 1:
+            if num_leaves == 0:
+                out = torch.zeros_like(q)
+                weights = torch.empty((*q.shape[:-1], 0), device=q.device, dtype=q.dtype)
+            else:
+                out = v.expand(q.shape[0], -1, -1, -1).contiguous()
+                weights = torch.ones((*q.shape[:-1], 1), device=q.device, dtype=q.dtype)
+            ctx.save_for_backward(q, k, v)
+            ctx.mark_non_differentiable(weights)
+            return out, weights
+        opts = TreeOptions(num_samples=int(num_samples), branching=2, leaf_block=1, tree_mode="nodekeys",
+                           causal=bool(is_causal), max_logit=float(max_logit), seed=int(seed), layout="lbhd")
+        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+        ctx.save_for_backward(q, k, v, weights, record)
+        ctx.opts = opts
+        ctx.mark_non_differentiable(weights)
+        return out, weights
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_weights):
+        del grad_weights
+        nones = (None,) * 6
+        if ctx.num_leaves <= 1:
+            q, k, v = ctx.saved_tensors
+            dv = torch.zeros_like(v)
+            if ctx.num_leaves == 1:
+                dv[0] = grad_out.float().sum(dim=0).to(v.dtype)
+            return (torch.zeros_like(q), torch.zeros_like(k), dv) + nones
+        q, k, v, weights, record = ctx.saved_tensors
+        dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, ctx.opts)
+        return (dq, dk, dv) + nones
+
+
+def record_views(q, k, v, opts: TreeOptions, record: torch.Tensor):
+    """``(leaves (B,L,H,S) int32, summaries (B*H, NS, D) float32)`` views of a record."""
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    prob = make_problem(q, k, v, opts)
+    lo = _lib.record_offset(prob, _lib.TA_REC_LEAVES)
+    so = _lib.record_offset(prob, _lib.TA_REC_SUMMARIES)
+    ns = _lib.record_offset(prob, _lib.TA_REC_NUM_ROWS)
+    n_leaf = prob.B * prob.L * prob.H * prob.num_samples
+    leaves = record[lo:lo + 4 * n_leaf].view(torch.int32).view(prob.B, prob.L, prob.H, prob.num_samples)
+    n_sum = prob.B * prob.H * ns * prob.D
+    summaries = record[so:so + 4 * n_sum].view(torch.float32).view(prob.B * prob.H, ns, prob.D)
+    return leaves, summaries
