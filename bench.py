@@ -1,0 +1,301 @@
+"""Benchmark: stochastic tree attention fwd+bwd on one MI355X.
+
+Workload (the config the metric is quoted on):
+B=2, L=16384, H=16, D=128, bf16, branching 4, leaf block 64, 16 paths per
+query, causal (bottom-right aligned), q/k/v/dout ~ N(0,1) from a seed-0
+torch.Generator (drawn in that order), Gumbel uniforms from the in-kernel
+counter RNG (seed 0).  One step = forward + backward through the public API
+(``tree_attention`` + ``out.backward``).
+
+Prints one JSON line with the headline figure (queries/s over the whole
+step), fwd/bwd ms, per-kernel-phase times measured with HIP events on the
+launch stream, the roofline of the dominant kernel, the CPU oracle timed on
+a bounded sample (``cpu_baseline``) and dense SDPA at the same shape.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    # name: B, L, H, D, dtype, b, LB, S, causal, kind
+    "C1": (1, 1024, 4, 64, "float32", 2, 16, 4, False, "normal"),
+    "C2": (4, 4096, 16, 64, "bfloat16", 2, 64, 8, False, "normal"),
+    "C3": (2, 16384, 16, 128, "bfloat16", 4, 64, 16, True, "normal"),
+    "C4": (1, 131072, 8, 128, "bfloat16", 2, 128, 16, False, "scaled"),
+}
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK = {"bfloat16": 2500.0, "float16": 2500.0, "float32": 157.3}  # dense TFLOP/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-sdpa", action="store_true", help="skip the dense SDPA baseline")
+    ap.add_argument("--phases-only", action="store_true", help="only run the per-phase loop (for profilers)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (scale reference for HBM counters)")
+    return ap.parse_args()
+
+
+def tree_units(B, L, H, D, e, b, LB, S):
+    """Algorithmic bytes / FLOPs per launch of each phase (uniforms generated in-kernel)."""
+    NL = L // LB
+    T = round(math.log(NL, b))
+    NS = b * (NL - 1) // (b - 1)
+    BLHD, BLHS = B * L * H * D, B * L * H * S
+    sums = NS * B * H * D * e
+    return dict(
+        T=T,
+        NS=NS,
+        pool_bytes=BLHD * e + sums,
+        sample_bytes=BLHD * e + sums + BLHS * 12,
+        sample_flops=BLHS * T * b * 2 * D,
+        leaf_fwd_flops=BLHS * 4 * LB * D,
+        leaf_bwd_flops=BLHS * 10 * LB * D,
+        fwd_bytes=4 * BLHD * e + BLHS * 8 + 2 * sums,
+        bwd_bytes=8 * BLHD * e + BLHS * 8 + 2 * sums,
+    )
+
+
+def read_traffic(kernel: str, config: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{config}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(cfg) -> dict:
+    """The float64 numpy oracle, 1 thread, on the last `nq` queries of one (batch, head)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import tree_oracle as O
+
+    B, L, H, D, dt, b, LB, S, causal, kind = cfg
+    nq = 2048 if L >= 4096 else L
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, nq, 1, D)).astype(np.float32)
+    k = rng.standard_normal((1, L, 1, D)).astype(np.float32)
+    v = rng.standard_normal((1, L, 1, D)).astype(np.float32)
+    do = rng.standard_normal((1, nq, 1, D)).astype(np.float32)
+    T = round(math.log(L // LB, b))
+    U = O.uniforms(0, (1, nq, 1, S, T, b))
+    mode = "natural" if b != 2 else "compat"
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        C = O.summaries(k.astype(np.float64), b, LB, mode)
+        out, w, idx, lp, _ = O.tree_forward(q, k, v, C, b, LB, U, causal)
+        dq, dC, dkl, dv = O.tree_backward(q, k, v, C, b, LB, idx, w, do, causal)
+        dk = dkl + O.pool_adjoint(dC, L, b, LB, mode)
+        dt_s = time.perf_counter() - t0
+    qps = nq / H / dt_s  # one query = all H heads
+    return {"value": qps, "unit": "queries/s", "cores": 1, "kind": "port",
+            "sample": f"numpy float64 oracle fwd+bwd, 1 thread, batch 0 head 0, last {nq} of {L} queries "
+                      f"(full {L}-token tree), {dt_s:.2f} s; scaled by 1/H to whole-query units"}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported",
+                          "n_gpus": args.gpus}))
+        return 2
+    import torch
+
+    import treeattention_amd as ta
+    from treeattention_amd import _lib
+    from treeattention_amd.function import TreeOptions, _prep, _strides, make_problem
+
+    cfg = CONFIGS[args.config]
+    B, L, H, D, dts, b, LB, S, causal, kind = cfg
+    dtype = getattr(torch, dts)
+    dev = torch.device("cuda:0")
+    mode = "natural" if b != 2 else "compat"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    shape = (B, L, H, D)
+    q, k, v, do = (torch.randn(shape, device=dev, dtype=dtype, generator=gen) for _ in range(4))
+    if kind == "scaled":
+        q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    kw = dict(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, seed=0)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = ta.tree_attention(q, k, v, causal, None, **kw)
+        out.backward(do)
+
+    def fwd():
+        with torch.no_grad():
+            ta.tree_attention(q, k, v, causal, None, **kw)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / n
+
+    res = {}
+    if not args.phases_only:
+        for _ in range(args.warmup):
+            step()
+        t0 = time.perf_counter()
+        step_ms = timed(step, args.steps)
+        wall = time.perf_counter() - t0
+        fwd_ms = timed(fwd, args.steps)
+        res.update(step_ms=step_ms, fwd_ms=fwd_ms, wall=wall)
+
+    # ---- per-phase timing through the C ABI (HIP events on the launch stream)
+    lib = _lib.load()
+    opts = TreeOptions(causal=causal, layout="bshd", **kw)
+    qd, kd, vd, dod = (_prep(x.detach()) for x in (q, k, v, do))
+    prob = make_problem(qd, kd, vd, opts)
+    rec_b, fws_b, bws_b = _lib.byte_sizes(prob)
+    out = torch.empty_like(qd)
+    w = torch.empty((B, L, H, S), device=dev, dtype=torch.float32)
+    prob.w_strides[:] = _strides(w, "bshd")
+    rec = torch.empty(rec_b, device=dev, dtype=torch.uint8)
+    fws = torch.empty(fws_b, device=dev, dtype=torch.uint8)
+    bws = torch.empty(bws_b, device=dev, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    pp = ctypes.byref(prob)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    phases = [
+        ("pool", lambda: lib.ta_pool(pp, kd.data_ptr(), rec.data_ptr(), stream)),
+        ("sample", lambda: lib.ta_sample(pp, qd.data_ptr(), None, 0, w.data_ptr(), rec.data_ptr(), stream)),
+        ("bucket", lambda: lib.ta_bucket(pp, rec.data_ptr(), stream)),
+        ("leaf_forward", lambda: lib.ta_leaf_forward(pp, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                                                     rec.data_ptr(), fws.data_ptr(), stream)),
+        ("leaf_backward", lambda: lib.ta_leaf_backward(pp, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                                       dod.data_ptr(), rec.data_ptr(), dv.data_ptr(),
+                                                       bws.data_ptr(), stream)),
+        ("tree_backward", lambda: lib.ta_tree_backward(pp, qd.data_ptr(), w.data_ptr(), rec.data_ptr(),
+                                                       dq.data_ptr(), dk.data_ptr(), bws.data_ptr(), stream)),
+    ]
+    n_ph = max(1, args.steps)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(n_ph)]
+    for it in range(1 + n_ph):  # first pass is warmup
+        for i, (name, fn) in enumerate(phases):
+            if it > 0:
+                evs[it - 1][i].record()
+            _lib.check(fn())
+        if it > 0:
+            evs[it - 1][-1].record()
+    torch.cuda.synchronize()
+    phase_ms = {name: sum(evs[j][i].elapsed_time(evs[j][i + 1]) for j in range(n_ph)) / n_ph
+                for i, (name, _) in enumerate(phases)}
+    if args.phases_only:
+        print(json.dumps({"phase_ms": phase_ms}))
+        return 0
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_calibration_bytes"] = 2 * src.numel() * src.element_size()
+
+    e = torch.finfo(dtype).bits // 8
+    u = tree_units(B, L, H, D, e, b, LB, S)
+    peak_t = MFMA_PEAK[dts]
+    kern = {
+        "leaf_backward": ("mfma", u["leaf_bwd_flops"]),
+        "leaf_forward": ("mfma", u["leaf_fwd_flops"]),
+        "sample": ("hbm", u["sample_bytes"]),
+        "pool": ("hbm", u["pool_bytes"]),
+    }
+    dom = max((k_ for k_ in kern), key=lambda k_: phase_ms[k_])
+    bound, units = kern[dom]
+    t_s = phase_ms[dom] / 1e3
+    if bound == "mfma":
+        achieved, peak, unit = units / t_s / 1e12, peak_t, "TFLOP/s"
+    else:
+        achieved, peak, unit = units / t_s / 1e9, HBM_PEAK_GBS, "GB/s"
+    roofline = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": read_traffic(dom, args.config), "kernel": dom}
+    per_phase = {}
+    for name, (bd, un) in kern.items():
+        ts = phase_ms[name] / 1e3
+        per_phase[name] = (f"{un / ts / 1e12:.1f} TFLOP/s ({un / ts / 1e12 / peak_t:.1%} of MFMA peak)" if bd == "mfma"
+                           else f"{un / ts / 1e9:.0f} GB/s ({un / ts / 1e9 / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    sdpa = None
+    if not args.no_sdpa and dtype != torch.float32:
+        try:
+            import torch.nn.functional as F
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+
+            qs, ks, vs = (x.detach().transpose(1, 2).requires_grad_(True) for x in (q, k, v))
+            gs = do.transpose(1, 2)
+
+            def sdpa_step():
+                qs.grad = ks.grad = vs.grad = None
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    o = F.scaled_dot_product_attention(qs, ks, vs, is_causal=causal)
+                o.backward(gs)
+
+            for _ in range(2):
+                sdpa_step()
+            sdpa = {"ms_per_step": round(timed(sdpa_step, max(3, args.steps // 2)), 3), "backend": "flash/efficient"}
+        except Exception as ex:  # no fused backend for this shape
+            sdpa = {"skipped": str(ex)[:200]}
+
+    cpu = None if args.no_cpu else cpu_baseline(cfg)
+    step_ms = res["step_ms"]
+    line = {
+        "metric": "tree-attn fwd+bwd ms & queries/s at L=16k bf16; achieved HBM GB/s %peak",
+        "value": round(B * L / (step_ms / 1e3), 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "fwd_ms": round(res["fwd_ms"], 4),
+        "bwd_ms": round(step_ms - res["fwd_ms"], 4),
+        "query_heads_per_s": round(B * L * H / (step_ms / 1e3), 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts.replace("bfloat16", "bf16").replace("float16", "fp16").replace("float32", "fp32"),
+        "data": "synthetic: q,k,v,dout ~ N(0,1) (torch.Generator seed 0), in-kernel Philox uniforms seed 0",
+        "config": {"workload": f"{args.config}: stochastic tree attention fwd+bwd", "batch": B, "seq_len": L,
+                   "heads": H, "head_dim": D, "branching": b, "leaf_block": LB, "num_samples": S,
+                   "causal": causal, "tree_mode": mode},
+        "phase_ms": {k_: round(v_, 4) for k_, v_ in phase_ms.items()},
+        "phase_roofline": per_phase,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "gpu_vs_cpu": round((B * L / (step_ms / 1e3)) / cpu["value"], 1) if cpu else None,
+        "sdpa_baseline": sdpa,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

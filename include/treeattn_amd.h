@@ -114,18 +114,39 @@ int ta_pool(const ta_problem* p, const void* k, void* record, void* stream);
 int ta_sample(const ta_problem* p, const void* q, const float* uniforms, uint64_t seed,
               float* weights, void* record, void* stream);
 
-/* Leaf-block attention and sample combine: out = sum_s w_s softmax(q K_blk^T) V_blk.
- * Buckets (query, leaf) pairs per leaf block, then MFMA tiles per block.
- * Needs ta_sample first.  Replaces weighted_value_sum_forward
- * (treeattn_cuda.cpp:91; weighted_value_sum.cu:8-47). */
+/* Groups every (query, distinct sampled leaf block) pair by leaf block (a
+ * stable counting sort per batch*head) into the record.  Needs ta_sample
+ * first.  Replaces the sampled-index bookkeeping the reference keeps in
+ * torch tensors (_autograd.py:685-700) with a per-block bucket that both the
+ * leaf forward and the atomic-free backward walk. */
+int ta_bucket(const ta_problem* p, void* record, void* stream);
+
+/* Leaf-block attention and sample combine: out = sum_s w_s softmax(q K_blk^T) V_blk,
+ * MFMA tiles per leaf-block bucket.  Needs ta_bucket first.  Replaces
+ * weighted_value_sum_forward (treeattn_cuda.cpp:91; weighted_value_sum.cu:8-47). */
 int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const void* v,
                     void* out, void* record, void* workspace, void* stream);
 
-/* Whole forward: ta_pool + ta_sample + ta_leaf_forward.  Replaces
+/* Whole forward: ta_pool + ta_sample + ta_bucket + ta_leaf_forward.  Replaces
  * _StochasticNonCausalTreeAttention.forward (_autograd.py:645-704). */
 int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
                const float* uniforms, uint64_t seed, void* out, float* weights,
                void* record, void* workspace, void* stream);
+
+/* Backward, leaf-block part: dv (complete), the leaf contribution to dk and
+ * per-pair dq and dout.o into `workspace`.  Replaces
+ * scatter_weighted_grad_v_forward (treeattn_cuda.cpp:290) and the value side
+ * of prepare_non_causal_backward (:176), without atomics. */
+int ta_leaf_backward(const ta_problem* p, const void* q, const void* k, const void* v,
+                     const void* grad_out, const void* record, void* dv, void* workspace, void* stream);
+
+/* Backward, tree part (after ta_leaf_backward with the same workspace):
+ * dq (complete) and dk (complete, including the summaries' adjoint).
+ * Replaces accumulate_qk_non_causal_all_depths_prepared_inplace
+ * (treeattn_cuda.cpp:211), the per-depth fallbacks (:321,:367) and the
+ * autograd of the Haar keys (_treeattn_common.py:70-86). */
+int ta_tree_backward(const ta_problem* p, const void* q, const float* weights, const void* record,
+                     void* dq, void* dk, void* workspace, void* stream);
 
 /* Whole backward from the forward's record: deterministic and atomic-free
  * dq, dk, dv (each fully overwritten).  Replaces

@@ -59,8 +59,11 @@ EXPORTS = (
     "ta_fill_uniforms",
     "ta_pool",
     "ta_sample",
+    "ta_bucket",
     "ta_leaf_forward",
     "ta_forward",
+    "ta_leaf_backward",
+    "ta_tree_backward",
     "ta_backward",
 )
 
@@ -88,6 +91,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_pool.argtypes = [P, vp, vp, vp]
     lib.ta_sample.restype = ctypes.c_int
     lib.ta_sample.argtypes = [P, vp, vp, ctypes.c_uint64, vp, vp, vp]
+    lib.ta_bucket.restype = ctypes.c_int
+    lib.ta_bucket.argtypes = [P, vp, vp]
+    lib.ta_leaf_backward.restype = ctypes.c_int
+    lib.ta_leaf_backward.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ta_tree_backward.restype = ctypes.c_int
+    lib.ta_tree_backward.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
     lib.ta_leaf_forward.restype = ctypes.c_int
     lib.ta_leaf_forward.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
     lib.ta_forward.restype = ctypes.c_int

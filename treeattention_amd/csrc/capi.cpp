@@ -229,6 +229,14 @@ int ta_sample(const ta_problem* p, const void* q, const float* uniforms, uint64_
   return launch_status(launch_sample(P, q, uniforms, seed, weights, (char*)record, (hipStream_t)stream), "sample");
 }
 
+int ta_bucket(const ta_problem* p, void* record, void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!record || !aligned16(record)) return fail(TA_ERR_INVALID, "record must be a 16-byte aligned device pointer");
+  return launch_status(launch_bucket(P, (char*)record, (hipStream_t)stream), "bucket");
+}
+
 int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const void* v, void* out, void* record,
                     void* workspace, void* stream) {
   Plan P;
@@ -238,10 +246,8 @@ int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const voi
   if (!q || !v || !out || !record || !workspace || (need_k && !k) || !aligned16(q) || !aligned16(v) ||
       !aligned16(out) || !aligned16(record) || !aligned16(workspace) || (need_k && !aligned16(k)))
     return fail(TA_ERR_INVALID, "q/k/v/out/record/workspace must be 16-byte aligned device pointers");
-  hipStream_t st = (hipStream_t)stream;
-  hipError_t e = launch_bucket(P, (char*)record, st);
-  if (e != hipSuccess) return launch_status(e, "bucket");
-  return launch_status(launch_leaf_fwd(P, q, k, v, out, (char*)record, (char*)workspace, st), "leaf_forward");
+  return launch_status(launch_leaf_fwd(P, q, k, v, out, (char*)record, (char*)workspace, (hipStream_t)stream),
+                       "leaf_forward");
 }
 
 int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v, const float* uniforms, uint64_t seed,
@@ -250,7 +256,40 @@ int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
   if (rc) return rc;
   rc = ta_sample(p, q, uniforms, seed, weights, record, stream);
   if (rc) return rc;
+  rc = ta_bucket(p, record, stream);
+  if (rc) return rc;
   return ta_leaf_forward(p, q, k, v, out, record, workspace, stream);
+}
+
+int ta_leaf_backward(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
+                     const void* record, void* dv, void* workspace, void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
+  if (!q || !v || !grad_out || !record || !dv || !workspace || (need_k && !k))
+    return fail(TA_ERR_INVALID, "NULL device pointer");
+  const void* al[] = {q, v, grad_out, record, dv, workspace};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  if (need_k && !aligned16(k)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  return launch_status(launch_leaf_bwd(P, q, k, v, grad_out, (const char*)record, dv, (char*)workspace,
+                                       (hipStream_t)stream),
+                       "leaf_backward");
+}
+
+int ta_tree_backward(const ta_problem* p, const void* q, const float* weights, const void* record, void* dq, void* dk,
+                     void* workspace, void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (!q || !weights || !record || !dq || !dk || !workspace) return fail(TA_ERR_INVALID, "NULL device pointer");
+  const void* al[] = {q, record, dq, dk, workspace};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  return launch_status(
+      launch_tree_bwd(P, q, weights, (const char*)record, dq, dk, (char*)workspace, (hipStream_t)stream),
+      "tree_backward");
 }
 
 int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
