@@ -208,17 +208,16 @@ def main() -> int:
     torch.cuda.synchronize()
     phase_ms = {name: sum(evs[j][i].elapsed_time(evs[j][i + 1]) for j in range(n_ph)) / n_ph
                 for i, (name, _) in enumerate(phases)}
-    if args.phases_only:
-        print(json.dumps({"phase_ms": phase_ms}))
-        return 0
-
     if args.copy_calibration:
-        src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16)
+        src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16)  # 1 GiB read + 1 GiB written
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        res["copy_calibration_bytes"] = 2 * src.numel() * src.element_size()
+        res["copy_calibration_bytes"] = src.numel() * src.element_size()
+    if args.phases_only:
+        print(json.dumps({"phase_ms": phase_ms}))
+        return 0
 
     e = torch.finfo(dtype).bits // 8
     u = tree_units(B, L, H, D, e, b, LB, S)

@@ -1,20 +1,23 @@
 // Bucketing of (query, distinct leaf block) pairs by leaf block, per
 // (batch, head): a stable counting sort so each leaf block's pairs are one
-// contiguous, deterministic run.  Every ancestor of a leaf block covers a
-// contiguous range of blocks, so the same order groups pairs by tree node at
-// every level.
+// contiguous, deterministic run in query order.  Every ancestor of a leaf
+// block covers a contiguous range of blocks, so the same order groups pairs
+// by tree node at every level.
 //
-// One wavefront scans a chunk of queries in position order; a query's
-// distinct blocks are different lanes with different counters, so LDS
-// counters give ranks that do not depend on scheduling.
+// A query lists each leaf block at most once, so within a chunk of
+// kQueryChunk queries the rank of (query l, block beta) in beta's run is the
+// number of earlier queries of the chunk that also picked beta: one bit per
+// (block, query) in LDS and a popcount give it without any ordering between
+// threads.
 #include "launch.h"
 
 namespace ta {
 
-constexpr int kWin = 8192;  // leaf-block counters held in LDS per pass
+constexpr int kWin = 2048;                 // leaf blocks per LDS window
+constexpr int kWords = kQueryChunk / 32;  // bitmask words per block
 
 struct BucketArgs {
-  int L, H, S, NL, qc, nchunk;
+  int L, H, S, NL, nchunk;
   const int* slot_leaf;
   const int* slot_count;
   int* hist;         // (BH, NL, nchunk)
@@ -22,36 +25,46 @@ struct BucketArgs {
   int* order;        // (BH, L*S)
 };
 
-// grid (nchunk, BH), block 64.  kScatter=false: counts per (block, chunk);
-// kScatter=true: writes order[] using the scanned hist as bases.
+// grid (nchunk, BH), block kQueryChunk (one thread per query of the chunk).
 template <bool kScatter>
-__global__ __launch_bounds__(64) void bucket_pass_kernel(BucketArgs a) {
-  __shared__ int cnt[kWin];
+__global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) {
+  __shared__ uint32_t bits[kWin * kWords];
   const int c = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
-  const int lane = threadIdx.x;
-  const int q0 = c * a.qc, q1 = min(a.L, q0 + a.qc);
+  const int tid = threadIdx.x;
+  const int l = c * kQueryChunk + tid;
+  const bool act = l < a.L;
+  const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+  const int n = act ? a.slot_count[qh] : 0;
+  const int* mine = a.slot_leaf + qh * a.S;
   const int64_t LS = (int64_t)a.L * a.S;
+  const uint32_t bit = 1u << (tid & 31);
+  const int word = tid >> 5;
   for (int w0 = 0; w0 < a.NL; w0 += kWin) {
     const int wn = min(kWin, a.NL - w0);
-    for (int i = lane; i < wn; i += 64) cnt[i] = 0;
+    for (int i = tid; i < wn * kWords; i += kQueryChunk) bits[i] = 0u;
     __syncthreads();
-    for (int l = q0; l < q1; ++l) {
-      const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-      const int n = a.slot_count[qh];
-      if (lane < n) {
-        const int beta = a.slot_leaf[qh * a.S + lane] - w0;
-        if (beta >= 0 && beta < wn) {
-          const int r = atomicAdd(&cnt[beta], 1);
-          if constexpr (kScatter) {
-            const int base = a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c];
-            a.order[(int64_t)bh * LS + base + r] = l * a.S + lane;
-          }
-        }
-      }
-      __syncthreads();
+    for (int u = 0; u < n; ++u) {
+      const int beta = mine[u] - w0;
+      if (beta >= 0 && beta < wn) atomicOr(&bits[beta * kWords + word], bit);
     }
+    __syncthreads();
     if constexpr (!kScatter) {
-      for (int i = lane; i < wn; i += 64) a.hist[((int64_t)bh * a.NL + w0 + i) * a.nchunk + c] = cnt[i];
+      for (int beta = tid; beta < wn; beta += kQueryChunk) {
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) cnt += __popc(bits[beta * kWords + k]);
+        a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c] = cnt;
+      }
+    } else {
+      for (int u = 0; u < n; ++u) {
+        const int beta = mine[u] - w0;
+        if (beta < 0 || beta >= wn) continue;
+        const uint32_t* bm = bits + beta * kWords;
+        int r = __popc(bm[word] & (bit - 1u));
+        for (int k = 0; k < word; ++k) r += __popc(bm[k]);
+        const int base = a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c];
+        a.order[(int64_t)bh * LS + base + r] = l * a.S + u;
+      }
     }
     __syncthreads();
   }
@@ -94,16 +107,15 @@ hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
   a.H = (int)P.H;
   a.S = (int)P.S;
   a.NL = P.geo.NL;
-  a.qc = P.qc;
   a.nchunk = P.nchunk;
   a.slot_leaf = (const int*)(rec + P.rec.slot_leaf);
   a.slot_count = (const int*)(rec + P.rec.slot_count);
   a.hist = (int*)(rec + P.rec.hist);
   a.block_start = (int*)(rec + P.rec.block_start);
   a.order = (int*)(rec + P.rec.order);
-  hipLaunchKernelGGL(bucket_pass_kernel<false>, dim3(P.nchunk, P.BH), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(bucket_pass_kernel<false>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
   hipLaunchKernelGGL(bucket_scan_kernel, dim3(P.BH), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(bucket_pass_kernel<true>, dim3(P.nchunk, P.BH), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(bucket_pass_kernel<true>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
   return hipGetLastError();
 }
 

@@ -56,7 +56,8 @@ int make_plan(const ta_problem* p, Plan* P) {
     return fail(TA_ERR_UNSUPPORTED, "head_dim must be one of 32, 64, 96, 128 (got %lld)", (long long)D);
   if (S < 1 || S > kMaxSamples)
     return fail(TA_ERR_UNSUPPORTED, "num_samples must be in [1, %d] (got %lld)", kMaxSamples, (long long)S);
-  if (b < 2 || b > 64) return fail(TA_ERR_INVALID, "branching must be in [2, 64] (got %lld)", (long long)b);
+  if (b < 2 || b > 64 || (b & (b - 1)))
+    return fail(TA_ERR_INVALID, "branching must be a power of two in [2, 64] (got %lld)", (long long)b);
   if (LB < 1 || LB > 128) return fail(TA_ERR_UNSUPPORTED, "leaf_block must be in [1, 128] (got %lld)", (long long)LB);
   if (N % LB) return fail(TA_ERR_INVALID, "N=%lld is not a multiple of leaf_block=%lld", (long long)N, (long long)LB);
   if (p->dtype != TA_F32 && p->dtype != TA_BF16 && p->dtype != TA_F16)
@@ -90,6 +91,8 @@ int make_plan(const ta_problem* p, Plan* P) {
   Geo& G = P->geo;
   memset(&G, 0, sizeof(G));
   G.b = (int)b; G.T = T; G.NL = (int)NL; G.LB = (int)LB;
+  G.lb = 0;
+  while ((1 << G.lb) < b) ++G.lb;
   G.pw[0] = 1;
   for (int i = 1; i <= T; ++i) G.pw[i] = G.pw[i - 1] * (int)b;
   G.off[0] = 0;
@@ -98,13 +101,14 @@ int make_plan(const ta_problem* p, Plan* P) {
   G.NS = G.off[T + 1];
   if ((int64_t)G.NS * D * 4 * P->BH > ((int64_t)1 << 40)) return fail(TA_ERR_UNSUPPORTED, "tree too large");
 
-  // bucketing chunks: keep the (block x chunk) count table modest
-  int qc = kQueryChunk;
-  while ((int64_t)NL * ((L + qc - 1) / qc) > ((int64_t)1 << 22) && qc < L) qc *= 2;
-  P->qc = qc;
-  P->nchunk = (int)((L + qc - 1) / qc);
+  // bucketing: one count per (leaf block, chunk of kQueryChunk queries)
+  P->qc = kQueryChunk;
+  P->nchunk = (int)((L + kQueryChunk - 1) / kQueryChunk);
+  if ((int64_t)NL * P->nchunk * P->BH > ((int64_t)1 << 29))
+    return fail(TA_ERR_UNSUPPORTED, "too many leaf blocks x query chunks for the bucket table (NL=%lld)",
+                (long long)NL);
   int ncol = 0;
-  for (int lam = 1; lam <= T; ++lam) ncol += (G.pw[lam] + kChunk - 1) / kChunk;
+  for (int lam = 1; lam <= T; ++lam) ncol += (G.pw[lam] + kDsumChunk - 1) / kDsumChunk;
   P->ncol = ncol;
   const int qtiles = (int)((L + kQueryTile - 1) / kQueryTile);
   int qsplit = ncol > 0 ? (int)((2048 + ncol * P->BH - 1) / (ncol * P->BH)) : 1;

@@ -20,6 +20,7 @@ constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 cov
 constexpr int kMaxSamples = 64;   // one wavefront lane per sample
 constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
 constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
+constexpr int kDsumChunk = 64;    // summary columns per workgroup of the summary-gradient kernel
 
 // Tree geometry.  Child summaries are stored level-major: level lam (1..T)
 // holds b^lam rows starting at off[lam], padded with zero rows to a multiple
@@ -27,7 +28,7 @@ constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
 // off[T+1] = NS.  Node i at depth d (0 <= i < b^d) has children rows
 // off[d+1] + b*i + j.
 struct Geo {
-  int b, T, NL, LB, NS;
+  int b, lb, T, NL, LB, NS;  // lb = log2(b): branching is a power of two
   int off[kMaxDepth + 2];
   int pw[kMaxDepth + 1];  // pw[i] = b^i
 };
@@ -174,6 +175,105 @@ __device__ __forceinline__ typename Mfma<E>::frag acc_operand(const f32x4 (&acc)
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+template <typename E> __device__ __forceinline__ typename Mfma<E>::frag zero_frag() {
+  typename Mfma<E>::frag r;
+  if constexpr (Mfma<E>::KPL == 1) {
+    r = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (E)0.f;
+  }
+  return r;
+}
+
+// A-operand fragments of one 16-row tile held in registers for the whole
+// reduction dimension D: lane (row l%16, k-group l/16) of row `row` (NULL ->
+// zeros, for rows past the end).
+template <typename E, int D>
+struct RowFrags {
+  typename Mfma<E>::frag f[D / Mfma<E>::K];
+  __device__ __forceinline__ void load(const E* row, int g) {
+#pragma unroll
+    for (int ks = 0; ks < D / Mfma<E>::K; ++ks)
+      f[ks] = row ? ld_frag(row + ks * Mfma<E>::K + Mfma<E>::KPL * g) : zero_frag<E>();
+  }
+};
+
+// X[16w + i][c] = A_i . B_row(c) for columns c < ncols (row row0 + c of the
+// row-major B matrix with row length D; tile columns past ncols read row
+// `rowmax`, a valid row whose results are never used), into X with row
+// stride xs.  With kLo the B rows are split hi + lo and both products
+// accumulate (float-accurate logits from 16-bit MFMA).  The next column
+// tile's B fragments are loaded while the current tile's MFMAs run.
+template <typename E, int D, bool kLo>
+__device__ __forceinline__ void mfma_rows(const RowFrags<E, D>& A, float* X, int xs, const E* hi, const E* lo,
+                                          int64_t row0, int ncols, int64_t rowmax, int lane, int w) {
+  using M = Mfma<E>;
+  constexpr int KS = D / M::K;
+  const int col = lane & 15, g = lane >> 4;
+  const int ntiles = (ncols + 15) >> 4;
+  typename M::frag bh[KS], bl[KS];
+  auto load = [&](int nt, typename M::frag(&h)[KS], typename M::frag(&l)[KS]) {
+    const int64_t rb = (nt * 16 + col < ncols ? row0 + nt * 16 + col : rowmax) * D + M::KPL * g;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      h[ks] = ld_frag(hi + rb + ks * M::K);
+      if constexpr (kLo) l[ks] = ld_frag(lo + rb + ks * M::K);
+    }
+  };
+  if (ntiles > 0) load(0, bh, bl);
+  for (int nt = 0; nt < ntiles; ++nt) {
+    typename M::frag nh[KS], nl[KS];
+    if (nt + 1 < ntiles) load(nt + 1, nh, nl);
+    f32x4 c = zero4();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      c = M::mma(A.f[ks], bh[ks], c);
+      if constexpr (kLo) c = M::mma(A.f[ks], bl[ks], c);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) X[(16 * w + 4 * g + r) * xs + nt * 16 + col] = c[r];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      bh[ks] = nh[ks];
+      if constexpr (kLo) bl[ks] = nl[ks];
+    }
+  }
+}
+
+// acc[0..8) += sum_{u < n} rows[u*stride .. +8) (E values, 16-byte aligned
+// when E is 16-bit), in u order; four rows' loads are in flight at once.
+template <typename E>
+__device__ __forceinline__ void sum_rows8(float* acc, const E* rows, int64_t stride, int n) {
+  int u = 0;
+  for (; u + 4 <= n; u += 4) {
+    float x[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const E* p = rows + (int64_t)(u + j) * stride;
+      if constexpr (sizeof(E) == 2) {
+        typedef __attribute__((ext_vector_type(8))) E v8;
+        const v8 v = *(const v8*)p;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[j][i] = (float)v[i];
+      } else {
+        const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+        x[j][0] = a.x; x[j][1] = a.y; x[j][2] = a.z; x[j][3] = a.w;
+        x[j][4] = b.x; x[j][5] = b.y; x[j][6] = b.z; x[j][7] = b.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += x[j][i];
+  }
+  for (; u < n; ++u) {
+    const E* p = rows + (int64_t)u * stride;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += (float)p[i];
+  }
+}
+
 // ------------------------------------------------------------ reductions ---
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -244,7 +344,7 @@ struct FwdWorkspaceLayout {
 struct BwdWorkspaceLayout {
   int64_t delta;     // float (B, L, H, S): dout . o per distinct leaf block
   int64_t dq_part;   // E (B, L, H, S, D): leaf dq per distinct leaf block
-  int64_t dlogp;     // float (B, L, H, S): gradient of each sample's log-prob
+  int64_t dlogp;     // float (B, L, H, S): gradient of each distinct leaf block's summed log-prob
   int64_t dk_leaf;   // float (B, N, H, D)
   int64_t dsum_part; // float (qsplit, BH, NS, D)
   int64_t dsum;      // float (BH, NS, D)

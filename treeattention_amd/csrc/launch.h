@@ -13,7 +13,7 @@ struct Plan {
   int esize;        // bytes per element of q/k/v
   int qc;           // queries per bucketing chunk
   int nchunk;       // bucketing chunks per (batch, head)
-  int ncol;         // child-summary chunks of kChunk columns over all levels
+  int ncol;         // child-summary chunks of kDsumChunk columns over all levels
   int qsplit;       // query splits of the summary-gradient kernel
   RecordLayout rec;
   FwdWorkspaceLayout fws;

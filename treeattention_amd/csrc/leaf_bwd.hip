@@ -17,7 +17,7 @@
 namespace ta {
 
 struct LeafBwdArgs {
-  int L, N, H, S, NL, LB, causal;
+  int B, L, N, H, S, NL, LB, causal;
   float scale, scale_log2;
   const void *q, *k, *v, *g;
   int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh, gsb, gsl, gsh;
@@ -49,21 +49,33 @@ __device__ __forceinline__ void zero8e(E* o) {
   }
 }
 
+// K^T is kept in LDS (for the dq product) when it fits next to the rest.
+template <int D, int LBP, int ES>
+struct BwdTile {
+  static constexpr int RS = D + 8, PS = 64 + 8, TS = LBP + 8;  // padded LDS row strides
+  static constexpr bool kKt = (LBP <= 64) || ES == 2 && D <= 64;
+  static constexpr int bytes = (2 * LBP * RS + 2 * 64 * RS + 2 * LBP * PS + (kKt ? D * TS : 0)) * ES + 64 * 4;
+};
+
 template <typename E, int D, int LBP>
 __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   using M = Mfma<E>;
-  constexpr int QT = 64;
+  using BT = BwdTile<D, LBP, (int)sizeof(E)>;
+  constexpr int QT = 64, RS = BT::RS, PS = BT::PS, TS = BT::TS;
   constexpr int NT = (LBP / 16) * (D / 16) / 4;  // dV / dK tiles per wave
   extern __shared__ __align__(16) char smem[];
-  E* Ks = (E*)smem;       // [LBP][D]
-  E* Vs = Ks + LBP * D;   // [LBP][D]
-  E* Qs = Vs + LBP * D;   // [QT][D]
-  E* Gs = Qs + QT * D;    // [QT][D]
-  E* Pt = Gs + QT * D;    // [LBP][QT]  (w P)^T
-  E* Zt = Pt + LBP * QT;  // [LBP][QT]  dz^T
-  int* ent_s = (int*)(Zt + LBP * QT);
+  E* Ks = (E*)smem;        // [LBP][RS]
+  E* Vs = Ks + LBP * RS;   // [LBP][RS]
+  E* Qs = Vs + LBP * RS;   // [QT][RS]
+  E* Gs = Qs + QT * RS;    // [QT][RS]
+  E* Pt = Gs + QT * RS;    // [LBP][PS]  (w P)^T
+  E* Zt = Pt + LBP * PS;   // [LBP][PS]  dz^T
+  E* Kt = Zt + LBP * PS;   // [D][TS]    K^T (if kKt)
+  int* ent_s = (int*)(Kt + (BT::kKt ? D * TS : 0));
 
-  const int beta = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  // blocks of all heads interleave so the heavy low blocks of causal runs start first
+  const int nbh = a.B * a.H;
+  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
@@ -77,10 +89,14 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   for (int e = tid; e < LBP * D / 8; e += 256) {
     const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
     const int64_t tok = (int64_t)beta * LB + key;
-    if (key < LB && k) mov8(Ks + key * D + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
-    else zero8e(Ks + key * D + c);
-    if (key < LB) mov8(Vs + key * D + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
-    else zero8e(Vs + key * D + c);
+    if (key < LB && k) mov8(Ks + key * RS + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+    else zero8e(Ks + key * RS + c);
+    if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+    else zero8e(Vs + key * RS + c);
+    if constexpr (BT::kKt) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Kt[(c + i) * TS + key] = Ks[key * RS + c + i];
+    }
   }
 
   f32x4 dvacc[NT], dkacc[NT];
@@ -96,11 +112,11 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
       const int ent = ent_s[r];
       if (ent >= 0) {
         const int l = ent / S;
-        mov8(Qs + r * D + c, q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + c);
-        mov8(Gs + r * D + c, go + bb * a.gsb + (int64_t)l * a.gsl + h * a.gsh + c);
+        mov8(Qs + r * RS + c, q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + c);
+        mov8(Gs + r * RS + c, go + bb * a.gsb + (int64_t)l * a.gsl + h * a.gsh + c);
       } else {
-        zero8e(Qs + r * D + c);
-        zero8e(Gs + r * D + c);
+        zero8e(Qs + r * RS + c);
+        zero8e(Gs + r * RS + c);
       }
     }
     __syncthreads();
@@ -116,10 +132,10 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
     for (int mt = 0; mt < LBP / 16; ++mt) {
       sacc[mt] = zero4();
       pacc[mt] = zero4();
-      const E* kp = Ks + (16 * mt + col) * D + M::KPL * g;
-      const E* vp = Vs + (16 * mt + col) * D + M::KPL * g;
-      const E* qp = Qs + qcol * D + M::KPL * g;
-      const E* gp = Gs + qcol * D + M::KPL * g;
+      const E* kp = Ks + (16 * mt + col) * RS + M::KPL * g;
+      const E* vp = Vs + (16 * mt + col) * RS + M::KPL * g;
+      const E* qp = Qs + qcol * RS + M::KPL * g;
+      const E* gp = Gs + qcol * RS + M::KPL * g;
 #pragma unroll
       for (int ks = 0; ks < D / M::K; ++ks) {
         sacc[mt] = M::mma(ld_frag(kp + ks * M::K), ld_frag(qp + ks * M::K), sacc[mt]);
@@ -169,8 +185,8 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
         const float p = sacc[mt][r];
         const float dz = wt * p * (pacc[mt][r] - delta);
         pacc[mt][r] = dz;
-        Pt[key * QT + qcol] = (E)(wt * p);
-        Zt[key * QT + qcol] = (E)dz;
+        Pt[key * PS + qcol] = (E)(wt * p);
+        Zt[key * PS + qcol] = (E)dz;
       }
     if (valid && g == 0) a.delta[qh * S + u] = delta;
 
@@ -178,10 +194,13 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
 #pragma unroll
     for (int md = 0; md < D / 16; ++md) {
       f32x4 o = zero4();
-      const E* kcol = Ks + 16 * md + col;
 #pragma unroll
-      for (int ks = 0; ks < LBP / M::K; ++ks)
-        o = M::mma(ld_frag_perm_strided<E>(kcol, D, ks, g), acc_operand<E>(pacc, ks), o);
+      for (int ks = 0; ks < LBP / M::K; ++ks) {
+        if constexpr (BT::kKt)
+          o = M::mma(ld_frag_perm(Kt + (16 * md + col) * TS, ks, g), acc_operand<E>(pacc, ks), o);
+        else
+          o = M::mma(ld_frag_perm_strided<E>(Ks + 16 * md + col, RS, ks, g), acc_operand<E>(pacc, ks), o);
+      }
       if (valid) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) dqp[16 * md + 4 * g + r] = (E)(o[r] * a.scale);
@@ -193,14 +212,14 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
     for (int t = 0; t < NT; ++t) {
       const int tile = w + 4 * t;
       const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
-      const E* pa = Pt + (16 * mk + col) * QT + M::KPL * g;
-      const E* za = Zt + (16 * mk + col) * QT + M::KPL * g;
-      const E* gb = Gs + (M::KPL * g) * D + 16 * nd + col;
-      const E* qb = Qs + (M::KPL * g) * D + 16 * nd + col;
+      const E* pa = Pt + (16 * mk + col) * PS + M::KPL * g;
+      const E* za = Zt + (16 * mk + col) * PS + M::KPL * g;
+      const E* gb = Gs + (M::KPL * g) * RS + 16 * nd + col;
+      const E* qb = Qs + (M::KPL * g) * RS + 16 * nd + col;
 #pragma unroll
       for (int ks = 0; ks < QT / M::K; ++ks) {
-        dvacc[t] = M::mma(ld_frag(pa + ks * M::K), ld_frag_strided(gb + ks * M::K * D, D), dvacc[t]);
-        dkacc[t] = M::mma(ld_frag(za + ks * M::K), ld_frag_strided(qb + ks * M::K * D, D), dkacc[t]);
+        dvacc[t] = M::mma(ld_frag(pa + ks * M::K), ld_frag_strided(gb + ks * M::K * RS, RS), dvacc[t]);
+        dkacc[t] = M::mma(ld_frag(za + ks * M::K), ld_frag_strided(qb + ks * M::K * RS, RS), dkacc[t]);
       }
     }
   }
@@ -223,14 +242,222 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   }
 }
 
+// Eight-wave variant: 128-pair tiles.  Phase A (each wave, its 16 pairs):
+// query and output-gradient rows come straight from global memory into MFMA
+// fragments (the next tile's are loaded while this one computes), then P,
+// delta, dz and the pair's dq.  Phase B (all waves): dV and dK over the 128
+// pairs from transposed LDS copies, every fragment a contiguous 16-byte read.
+template <int D, int LBP, int ES>
+struct Bwd8Tile {
+  static constexpr int QT = 128;
+  static constexpr int RS = D + 8, TS = LBP + 8, PS = QT + 8;
+  static constexpr int bytes = (2 * LBP * RS + D * TS + 2 * D * PS + 2 * LBP * PS) * ES;
+};
+
+template <typename E, int D, int LBP>
+__global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
+  using M = Mfma<E>;
+  using BT = Bwd8Tile<D, LBP, (int)sizeof(E)>;
+  constexpr int QT = BT::QT, RS = BT::RS, TS = BT::TS, PS = BT::PS;
+  constexpr int NW = 8;
+  constexpr int NT = (LBP / 16) * (D / 16) / NW;  // dV / dK tiles per wave
+  static_assert(NT >= 1 && (LBP / 16) * (D / 16) % NW == 0, "tile split");
+  extern __shared__ __align__(16) char smem[];
+  E* Ks = (E*)smem;        // [LBP][RS]
+  E* Vs = Ks + LBP * RS;   // [LBP][RS]
+  E* Kt = Vs + LBP * RS;   // [D][TS]
+  E* Qt = Kt + D * TS;     // [D][PS]   Q^T of the tile
+  E* Gt = Qt + D * PS;     // [D][PS]   dout^T of the tile
+  E* Pt = Gt + D * PS;     // [LBP][PS] (w P)^T
+  E* Zt = Pt + LBP * PS;   // [LBP][PS] dz^T
+
+  const int nbh = a.B * a.H;
+  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
+  const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
+  const int start = bs[beta], end = bs[beta + 1];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int LB = a.LB, S = a.S;
+  const int64_t LS = (int64_t)a.L * S;
+  const E* q = (const E*)a.q;
+  const E* k = (const E*)a.k;
+  const E* v = (const E*)a.v;
+  const E* go = (const E*)a.g;
+
+  for (int e = tid; e < LBP * D / 8; e += NW * 64) {
+    const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+    const int64_t tok = (int64_t)beta * LB + key;
+    if (key < LB && k) mov8(Ks + key * RS + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+    else zero8e(Ks + key * RS + c);
+    if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+    else zero8e(Vs + key * RS + c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Kt[(c + i) * TS + key] = Ks[key * RS + c + i];
+  }
+  __syncthreads();
+
+  f32x4 dvacc[NT], dkacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) { dvacc[t] = zero4(); dkacc[t] = zero4(); }
+
+  const int* ord = a.order + (int64_t)bh * LS;
+  const int pcol = 16 * w + col;  // this lane's pair column within the tile
+  int ent = start + pcol < end ? ord[start + pcol] : -1;
+  RowFrags<E, D> qf, gf;
+  {
+    const int64_t lo = ent >= 0 ? (int64_t)(ent / S) : 0;
+    qf.load(ent >= 0 ? q + bb * a.qsb + lo * a.qsl + h * a.qsh : nullptr, g);
+    gf.load(ent >= 0 ? go + bb * a.gsb + lo * a.gsl + h * a.gsh : nullptr, g);
+  }
+  for (int t0 = start; t0 < end; t0 += QT) {
+    const int cur = ent;
+    const RowFrags<E, D> qc = qf, gc = gf;
+    {
+      const int t1 = t0 + QT;
+      ent = t1 + pcol < end ? ord[t1 + pcol] : -1;
+      const int64_t lo = ent >= 0 ? (int64_t)(ent / S) : 0;
+      qf.load(ent >= 0 ? q + bb * a.qsb + lo * a.qsl + h * a.qsh : nullptr, g);
+      gf.load(ent >= 0 ? go + bb * a.gsb + lo * a.gsl + h * a.gsh : nullptr, g);
+    }
+    const bool valid = cur >= 0;
+    const int l = valid ? cur / S : 0, u = valid ? cur - l * S : 0;
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+
+    // ---- phase A: this wave's 16 pairs
+    f32x4 sacc[LBP / 16], pacc[LBP / 16];
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt) {
+      sacc[mt] = zero4();
+      pacc[mt] = zero4();
+      const E* kp = Ks + (16 * mt + col) * RS + M::KPL * g;
+      const E* vp = Vs + (16 * mt + col) * RS + M::KPL * g;
+#pragma unroll
+      for (int ks = 0; ks < D / M::K; ++ks) {
+        sacc[mt] = M::mma(ld_frag(kp + ks * M::K), qc.f[ks], sacc[mt]);
+        pacc[mt] = M::mma(ld_frag(vp + ks * M::K), gc.f[ks], pacc[mt]);
+      }
+    }
+    const int kmax = valid ? (a.causal ? min(LB, l + (a.N - a.L) - beta * LB + 1) : LB) : 0;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sv = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
+        sacc[mt][r] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = (16 * mt + 4 * g + r) < kmax ? exp2f(sacc[mt][r] - mx) : 0.f;
+        sacc[mt][r] = pv;
+        sum += pv;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    float delta = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sacc[mt][r] *= inv;
+        delta += sacc[mt][r] * pacc[mt][r];
+      }
+    delta += __shfl_xor(delta, 16, 64);
+    delta += __shfl_xor(delta, 32, 64);
+    const float wt = valid ? a.slot_weight[qh * S + u] : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pacc[mt][r] = wt * sacc[mt][r] * (pacc[mt][r] - delta);
+    if (valid && g == 0) a.delta[qh * S + u] = delta;
+
+    E* dqp = (E*)a.dq_part + (qh * S + u) * D;
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md) {
+      f32x4 o = zero4();
+#pragma unroll
+      for (int ks = 0; ks < LBP / M::K; ++ks)
+        o = M::mma(ld_frag_perm(Kt + (16 * md + col) * TS, ks, g), acc_operand<E>(pacc, ks), o);
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dqp[16 * md + 4 * g + r] = (E)(o[r] * a.scale);
+      }
+    }
+
+    __syncthreads();  // phase B of the previous tile is done with the staging buffers
+#pragma unroll
+    for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * mt + 4 * g + r;
+        Pt[key * PS + pcol] = (E)(wt * sacc[mt][r]);
+        Zt[key * PS + pcol] = (E)pacc[mt][r];
+      }
+#pragma unroll
+    for (int ks = 0; ks < D / M::K; ++ks) {
+      if constexpr (M::KPL == 1) {
+        Qt[(ks * M::K + g) * PS + pcol] = qc.f[ks];
+        Gt[(ks * M::K + g) * PS + pcol] = gc.f[ks];
+      } else {
+#pragma unroll
+        for (int i = 0; i < M::KPL; ++i) {
+          Qt[(ks * M::K + M::KPL * g + i) * PS + pcol] = qc.f[ks][i];
+          Gt[(ks * M::K + M::KPL * g + i) * PS + pcol] = gc.f[ks][i];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- phase B: dV, dK over the tile's 128 pairs
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = w + NW * t;
+      const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
+      const E* pa = Pt + (16 * mk + col) * PS + M::KPL * g;
+      const E* za = Zt + (16 * mk + col) * PS + M::KPL * g;
+      const E* gb = Gt + (16 * nd + col) * PS + M::KPL * g;
+      const E* qb = Qt + (16 * nd + col) * PS + M::KPL * g;
+#pragma unroll
+      for (int ks = 0; ks < QT / M::K; ++ks) {
+        dvacc[t] = M::mma(ld_frag(pa + ks * M::K), ld_frag(gb + ks * M::K), dvacc[t]);
+        dkacc[t] = M::mma(ld_frag(za + ks * M::K), ld_frag(qb + ks * M::K), dkacc[t]);
+      }
+    }
+  }
+
+  E* dv = (E*)a.dv;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = w + NW * t;
+    const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = 16 * mk + 4 * g + r;
+      if (key < LB) {
+        const int64_t tok = (int64_t)beta * LB + key;
+        const int d = 16 * nd + col;
+        dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[t][r];
+        if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[t][r] * a.scale;
+      }
+    }
+  }
+}
+
 template <typename E, int D, int LBP>
 static int bwd_smem_t() {
-  return (2 * LBP * D + 2 * 64 * D + 2 * LBP * 64) * (int)sizeof(E) + 64 * 4;
+  return BwdTile<D, LBP, (int)sizeof(E)>::bytes;
 }
 
 int leaf_bwd_smem(const Plan& P) {
-  const int LBP = padded_keys(P.geo.LB);
-  const int s = (2 * LBP * (int)P.D + 2 * 64 * (int)P.D + 2 * LBP * 64) * P.esize + 64 * 4;
+  const int D = (int)P.D, LBP = padded_keys(P.geo.LB), ES = P.esize;
+  const bool kt = (LBP <= 64) || (ES == 2 && D <= 64);
+  const int s = (2 * LBP * (D + 8) + 2 * 64 * (D + 8) + 2 * LBP * 72 + (kt ? D * (LBP + 8) : 0)) * ES + 64 * 4;
   return s <= 160 * 1024 ? s : -1;
 }
 
@@ -238,6 +465,7 @@ template <typename E, int D, int LBP>
 static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, const void* v, const void* g,
                                 const char* rec, void* dv, char* ws, hipStream_t st) {
   LeafBwdArgs a;
+  a.B = (int)P.B;
   a.L = (int)P.L;
   a.N = (int)P.N;
   a.H = (int)P.H;
@@ -263,11 +491,20 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.dq_part = ws + P.bws.dq_part;
   a.dv = dv;
   a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
-  const int smem = bwd_smem_t<E, D, LBP>();
-  hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((leaf_bwd_kernel<E, D, LBP>), dim3(P.geo.NL, P.BH), dim3(256), smem, st, a);
+  const unsigned grid = (unsigned)(P.BH * P.geo.NL);
+  constexpr int smem8 = Bwd8Tile<D, LBP, (int)sizeof(E)>::bytes;
+  if constexpr (LBP <= 64 && smem8 <= 160 * 1024 && (LBP / 16) * (D / 16) % 8 == 0) {
+    hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd8_kernel<E, D, LBP>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem8);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((leaf_bwd8_kernel<E, D, LBP>), dim3(grid), dim3(512), smem8, st, a);
+  } else {
+    const int smem = bwd_smem_t<E, D, LBP>();
+    hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((leaf_bwd_kernel<E, D, LBP>), dim3(grid), dim3(256), smem, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -15,7 +15,7 @@
 namespace ta {
 
 struct LeafFwdArgs {
-  int L, H, S, NL, LB, causal, coff;
+  int B, L, H, S, NL, LB, causal, coff;
   float scale_log2;
   const void *q, *k, *v;
   int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh;
@@ -38,14 +38,14 @@ __device__ __forceinline__ void load8(E* o, const E* p) {
 template <typename E, int D, int LBP>
 __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
   using M = Mfma<E>;
-  constexpr int QT = 64;
+  constexpr int KS = D + 8, VS = LBP + 8;  // padded LDS row strides
   extern __shared__ __align__(16) char smem[];
-  E* Ks = (E*)smem;        // [LBP][D]
-  E* Vt = Ks + LBP * D;    // [D][LBP]
-  E* Qs = Vt + D * LBP;    // [QT][D]
-  int* ent_s = (int*)(Qs + QT * D);
+  E* Ks = (E*)smem;         // [LBP][KS]
+  E* Vt = Ks + LBP * KS;    // [D][VS]
 
-  const int beta = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  // blocks of all heads interleave so the heavy low blocks of causal runs start first
+  const int nbh = a.B * a.H;
+  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
   if (start >= end) return;
@@ -67,43 +67,36 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
       if (k) load8(kv, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
       load8(vv, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
     }
-    load8(Ks + key * D + c, kv);
+    load8(Ks + key * KS + c, kv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) Vt[(c + i) * LBP + key] = vv[i];
+    for (int i = 0; i < 8; ++i) Vt[(c + i) * VS + key] = vv[i];
   }
+  __syncthreads();
 
-  for (int t0 = start; t0 < end; t0 += QT) {
-    __syncthreads();
-    if (tid < QT) ent_s[tid] = (t0 + tid < end) ? a.order[(int64_t)bh * LS + t0 + tid] : -1;
-    __syncthreads();
-    for (int e = tid; e < QT * D / 8; e += 256) {
-      const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
-      const int ent = ent_s[r];
-      if (ent >= 0) {
-        const int l = ent / S;
-        load8(Qs + r * D + c, q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + c);
-      } else {
-        alignas(16) E z[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) z[i] = (E)0.f;
-        load8(Qs + r * D + c, z);
-      }
-    }
-    __syncthreads();
+  // Each wave walks its own 16-pair tiles (tile j of the bucket goes to wave
+  // j % 4); no workgroup barrier inside the loop.  The next tile's pair ids
+  // and query rows are loaded while the current tile computes.
+  const int* ord = a.order + (int64_t)bh * LS;
+  int t0 = start + 16 * w;
+  int ent = t0 + col < end ? ord[t0 + col] : -1;
+  RowFrags<E, D> qf;
+  qf.load(ent >= 0 ? q + bb * a.qsb + (int64_t)(ent / S) * a.qsl + h * a.qsh : nullptr, g);
+  for (; t0 < end; t0 += 64) {
+    const int cur = ent;
+    RowFrags<E, D> qc = qf;
+    const int t1 = t0 + 64;
+    ent = t1 + col < end ? ord[t1 + col] : -1;
+    qf.load(ent >= 0 ? q + bb * a.qsb + (int64_t)(ent / S) * a.qsl + h * a.qsh : nullptr, g);
 
-    const int qcol = 16 * w + col;
-    const int ent = ent_s[qcol];
-    const bool valid = ent >= 0;
-    const int l = valid ? ent / S : 0, u = valid ? ent - l * S : 0;
-
+    const bool valid = cur >= 0;
+    const int l = valid ? cur / S : 0, u = valid ? cur - l * S : 0;
     f32x4 sacc[LBP / 16];
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt) {
       sacc[mt] = zero4();
-      const E* ap = Ks + (16 * mt + col) * D + M::KPL * g;
-      const E* bp = Qs + qcol * D + M::KPL * g;
+      const E* ap = Ks + (16 * mt + col) * KS + M::KPL * g;
 #pragma unroll
-      for (int ks = 0; ks < D / M::K; ++ks) sacc[mt] = M::mma(ld_frag(ap + ks * M::K), ld_frag(bp + ks * M::K), sacc[mt]);
+      for (int ks = 0; ks < D / M::K; ++ks) sacc[mt] = M::mma(ld_frag(ap + ks * M::K), qc.f[ks], sacc[mt]);
     }
     // keys < kmax are visible to this query
     const int kmax = valid ? (a.causal ? min(LB, l + a.coff - beta * LB + 1) : LB) : 0;
@@ -137,7 +130,7 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
 #pragma unroll
     for (int md = 0; md < D / 16; ++md) {
       f32x4 o = zero4();
-      const E* vrow = Vt + (16 * md + col) * LBP;
+      const E* vrow = Vt + (16 * md + col) * VS;
 #pragma unroll
       for (int ks = 0; ks < LBP / M::K; ++ks) o = M::mma(ld_frag_perm(vrow, ks, g), acc_operand<E>(sacc, ks), o);
       if (valid) {
@@ -153,31 +146,30 @@ template <typename E, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
                                                       E* __restrict__ out, int L, int H, int S, int64_t nqh,
                                                       int64_t osb, int64_t osl, int64_t osh) {
-  constexpr int TPQ = D / 4;
+  constexpr int TPQ = D / 8;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t qh = gid / TPQ;
   if (qh >= nqh) return;
   const int part = (int)(gid - qh * TPQ);
-  const int n = slot_count[qh];
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const E* p = partial + qh * S * D + 4 * part;
-  for (int u = 0; u < n; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += tof(p[(int64_t)u * D + i]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  sum_rows8(acc, partial + qh * S * D + 8 * part, D, slot_count[qh]);
   const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
-  E* o = out + bb * osb + l * osl + h * osh + 4 * part;
+  E* o = out + bb * osb + l * osl + h * osh + 8 * part;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = (E)acc[i];
+  for (int i = 0; i < 8; ++i) o[i] = (E)acc[i];
+}
+
+static int fwd_smem(int D, int LBP, int es) {
+  return (LBP * (D + 8) + D * (LBP + 8)) * es;
 }
 
 template <typename E, int D, int LBP>
 static int fwd_smem_t() {
-  return (2 * LBP * D + 64 * D) * (int)sizeof(E) + 64 * 4;
+  return fwd_smem(D, LBP, (int)sizeof(E));
 }
 
 int leaf_fwd_smem(const Plan& P) {
-  const int LBP = padded_keys(P.geo.LB);
-  const int s = (2 * LBP * (int)P.D + 64 * (int)P.D) * P.esize + 64 * 4;
+  const int s = fwd_smem((int)P.D, padded_keys(P.geo.LB), P.esize);
   return s <= 160 * 1024 ? s : -1;
 }
 
@@ -185,6 +177,7 @@ template <typename E, int D, int LBP>
 static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
                                 char* ws, hipStream_t st) {
   LeafFwdArgs a;
+  a.B = (int)P.B;
   a.L = (int)P.L;
   a.H = (int)P.H;
   a.S = (int)P.S;
@@ -207,9 +200,9 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(P.geo.NL, P.BH), dim3(256), smem, st, a);
+  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3((unsigned)(P.BH * P.geo.NL)), dim3(256), smem, st, a);
   const int64_t nqh = P.B * P.L * P.H;
-  const int64_t nthr = nqh * (D / 4);
+  const int64_t nthr = nqh * (D / 8);
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
                      (const E*)a.partial, (const int*)(rec + P.rec.slot_count), (E*)out, (int)P.L, (int)P.H,
                      (int)P.S, nqh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2]);

@@ -37,52 +37,9 @@ struct SampleArgs {
 };
 
 constexpr int kDoneBit = 1 << 30;
+constexpr int kXS = kChunk + 4;  // padded row stride (floats) of the logit tile
 
 __device__ __forceinline__ float clampf(float x, float m) { return fminf(fmaxf(x, -m), m); }
-
-template <typename E>
-__device__ __forceinline__ void copy8(E* dst, const E* src) {
-  if constexpr (sizeof(E) == 2) {
-    *(uint4*)dst = *(const uint4*)src;
-  } else {
-    *(float4*)dst = *(const float4*)src;
-    *(float4*)(dst + 4) = *(const float4*)(src + 4);
-  }
-}
-template <typename E>
-__device__ __forceinline__ void zero8(E* dst) {
-  if constexpr (sizeof(E) == 2) {
-    *(uint4*)dst = make_uint4(0, 0, 0, 0);
-  } else {
-    *(float4*)dst = make_float4(0, 0, 0, 0);
-    *(float4*)(dst + 4) = make_float4(0, 0, 0, 0);
-  }
-}
-
-// Child logits of columns [c0, c0+ncols) of level lam for the 64 queries in
-// Qs, raw (unclamped), into Xs[64][kChunk].  Wave w owns rows 16w..16w+15.
-// hi + lo parts for 16-bit inputs; the float summaries for float inputs.
-template <typename E, int D, bool kLo>
-__device__ __forceinline__ void child_logits(const E* Qs, float* Xs, const E* hi, const E* lo,
-                                             int64_t row0, int ncols, int lane, int w) {
-  using M = Mfma<E>;
-  const int col = lane & 15, g = lane >> 4;
-  const int ntiles = (ncols + 15) >> 4;
-  for (int nt = 0; nt < ntiles; ++nt) {
-    f32x4 c = zero4();
-    const E* bh_ = hi + (row0 + nt * 16 + col) * D + M::KPL * g;
-    const E* bl_ = lo + (row0 + nt * 16 + col) * D + M::KPL * g;
-    const E* a_ = Qs + (16 * w + col) * D + M::KPL * g;
-#pragma unroll
-    for (int ks = 0; ks < D / M::K; ++ks) {
-      const auto a = ld_frag(a_ + ks * M::K);
-      c = M::mma(a, ld_frag(bh_ + ks * M::K), c);
-      if constexpr (kLo) c = M::mma(a, ld_frag(bl_ + ks * M::K), c);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[(16 * w + 4 * g + r) * kChunk + nt * 16 + col] = c[r];
-  }
-}
 
 template <typename E, int D>
 __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
@@ -91,24 +48,22 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
   const int l0 = blockIdx.x * kQueryTile;
   const int nq = min(kQueryTile, a.L - l0);
-  const int S = a.S, T = G.T, b = G.b;
+  const int S = a.S, T = G.T, b = G.b, lb = G.lb;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t rows = G.NS;
+  constexpr bool kLo = sizeof(E) == 2;
 
-  E* Qs = (E*)smem;
-  float* Xs = (float*)(Qs + kQueryTile * D);
-  int* node = (int*)(Xs + kQueryTile * kChunk);
+  float* Xs = (float*)smem;
+  int* node = (int*)(Xs + kQueryTile * kXS);
   float* acc = (float*)(node + kQueryTile * S);
   float* logA = acc + kQueryTile * S;        // [64][T+1]
   float* xb = logA + kQueryTile * (T + 1);   // [64][T*b]
 
-  const E* q = (const E*)a.q;
-  for (int e = tid; e < kQueryTile * D / 8; e += 256) {
-    const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
-    if (r < nq)
-      copy8(Qs + r * D + c, q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh + c);
-    else
-      zero8(Qs + r * D + c);
+  // this wave's 16 query rows stay in registers as MFMA A fragments
+  RowFrags<E, D> qf;
+  {
+    const int r = 16 * w + (lane & 15);
+    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
   }
   for (int e = tid; e < kQueryTile * S; e += 256) {
     node[e] = 0;
@@ -116,30 +71,40 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   }
   __syncthreads();
 
+  const E* hi = (const E*)(sizeof(E) == 2 ? a.sum_hi : (const void*)a.sum32);
+  const E* lo = (const E*)a.sum_lo;
+
   // Causal: allowed log-mass of each boundary-path node, bottom-up:
-  // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.
+  // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.  The boundary nodes of
+  // consecutive queries form one contiguous node range per depth, so their
+  // child logits come from the same MFMA tile as the walk's.
   if (a.causal && T > 0) {
     const int nb = T * b;
-    for (int e = tid; e < kQueryTile * nb; e += 256) {
-      const int qi = e / nb, dj = e - qi * nb;
-      const int d = dj / b, j = dj - d * b;
-      float x = 0.f;
-      if (qi < nq) {
-        const int blk = (l0 + qi + a.coff) / G.LB;
-        const int row = G.off[d + 1] + b * (blk / G.pw[T - d]) + j;
-        const float* c = a.sum32 + ((int64_t)bh * rows + row) * D;
-        const E* qq = Qs + qi * D;
-        for (int t = 0; t < D; ++t) x += tof(qq[t]) * c[t];
+    const int blk_lo = (l0 + a.coff) / G.LB, blk_hi = (l0 + nq - 1 + a.coff) / G.LB;
+    for (int d = 0; d < T; ++d) {
+      const int sh = lb * (T - d);
+      const int c0 = (blk_lo >> sh) << lb;
+      const int ncols = (((blk_hi >> sh) + 1) << lb) - c0;
+      for (int cc = 0; cc < ncols; cc += kChunk) {
+        const int nc = min(kChunk, ncols - cc);
+        const int64_t r0 = (int64_t)bh * rows + G.off[d + 1] + c0 + cc;
+        mfma_rows<E, D, kLo>(qf, Xs, kXS, hi, lo, r0, nc, r0, lane, w);
+        __syncthreads();
+        for (int qi = tid; qi < nq; qi += 256) {
+          const int blk = (l0 + qi + a.coff) / G.LB;
+          const int col = ((blk >> sh) << lb) - c0 - cc;
+          if (col >= 0 && col < nc)
+            for (int j = 0; j < b; ++j) xb[qi * nb + d * b + j] = clampf(Xs[qi * kXS + col + j], a.maxhalf);
+        }
+        __syncthreads();
       }
-      xb[e] = clampf(x, a.maxhalf);
     }
-    __syncthreads();
     if (tid < nq) {
       const int blk = (l0 + tid + a.coff) / G.LB;
       float* la = logA + tid * (T + 1);
       la[T] = 0.f;
       for (int d = T - 1; d >= 0; --d) {
-        const int js = (blk / G.pw[T - 1 - d]) % b;
+        const int js = (blk >> (lb * (T - 1 - d))) & (b - 1);
         const float* xs = xb + tid * nb + d * b;
         float mx = -__builtin_inff();
         for (int j = 0; j < b; ++j) mx = fmaxf(mx, xs[j]);
@@ -157,24 +122,22 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     __syncthreads();
   }
 
-  const E* hi = (const E*)(sizeof(E) == 2 ? a.sum_hi : (const void*)a.sum32);
-  const E* lo = (const E*)a.sum_lo;
   for (int d = 0; d < T; ++d) {
     const int lam = d + 1, lvl = G.pw[lam];
     for (int c0 = 0; c0 < lvl; c0 += kChunk) {
       const int ncols = min(kChunk, lvl - c0);
-      child_logits<E, D, sizeof(E) == 2>(Qs, Xs, hi, lo, (int64_t)bh * rows + G.off[lam] + c0, ncols,
-                                         lane, w);
+      const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
+      mfma_rows<E, D, kLo>(qf, Xs, kXS, hi, lo, r0, ncols, r0, lane, w);
       __syncthreads();
       for (int it = tid; it < kQueryTile * S; it += 256) {
         const int qi = it / S;
         if (qi >= nq) continue;
         const int i = node[it];
         if (i & kDoneBit) continue;
-        const int base = b * i - c0;
+        const int base = (i << lb) - c0;
         if (base < 0 || base >= ncols) continue;
         const int s = it - qi * S;
-        const float* xr = Xs + qi * kChunk + base;
+        const float* xr = Xs + qi * kXS + base;
         float mx = -__builtin_inff();
         for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
         float se = 0.f;
@@ -185,9 +148,9 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
         float la_d = 0.f, la_c = 0.f;
         if (a.causal) {
           const int blk = (l0 + qi + a.coff) / G.LB;
-          if (blk / G.pw[T - d] == i) {
+          if ((blk >> (lb * (T - d))) == i) {
             onb = true;
-            js = (blk / G.pw[T - 1 - d]) % b;
+            js = (blk >> (lb * (T - 1 - d))) & (b - 1);
             la_d = logA[qi * (T + 1) + d];
             la_c = logA[qi * (T + 1) + d + 1];
           }
@@ -224,7 +187,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
             bl = lp;
           }
         }
-        node[it] = (b * i + bj) | kDoneBit;
+        node[it] = ((i << lb) + bj) | kDoneBit;
         acc[it] += bl;
       }
       __syncthreads();
@@ -272,7 +235,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
 
 int sample_smem(const Plan& P) {
   const int T = P.geo.T, b = P.geo.b;
-  return kQueryTile * (int)P.D * P.esize + kQueryTile * kChunk * 4 + kQueryTile * (int)P.S * 8 +
+  return kQueryTile * kXS * 4 + kQueryTile * (int)P.S * 8 +
          kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
 }
 

@@ -1,24 +1,33 @@
 // K4b: tree part of the backward (the reference's per-depth grad_logit and
 // q/k accumulation, _autograd.py:789-856 and
-// accumulate_qk_non_causal_all_depths_prepared.cu:104-161), deterministic:
+// accumulate_qk_non_causal_all_depths_prepared.cu:104-161), deterministic.
 //
-//  * dlogp_s = w_s (delta_s - sum_s' w_s' delta_s'), delta from the leaf
-//    backward (softmax-over-samples adjoint, _autograd.py:791-794);
-//  * at depth d a sample at node i with chosen child j* contributes
-//    dx_j = dlogp_s (1[j = j*] - p_j) to every child logit j of i (zero where
-//    the logit was clamped); per query these are summed into G (queries x
-//    child summaries of one column chunk) in LDS;
-//  * tree_dq_kernel:   dq = sum_pairs dq_pair + sum_chunks G C_chunk     (MFMA)
-//  * tree_dsum_kernel: dC_chunk = sum_queries G^T Q per query split      (MFMA)
-//    and dsum_reduce_kernel adds the splits in order;
-//  * pool_adjoint_kernel: dk = dk_leaf + (summaries map)^T dC, which for
-//    compat summaries is the transpose of the reference's Haar keys
-//    (_treeattn_common.py:70-86).
+// Per sample s, dlogp_s = w_s (delta_s - sum_s' w_s' delta_s') (softmax over
+// samples, _autograd.py:791-794).  Samples that picked the same leaf block u
+// share their whole path, so only the per-block sum matters:
+//   dl_u = sum_{s->u} dlogp_s = W_u (delta_u - sum_u' W_u' delta_u'),
+// W_u the summed sample weight.  At depth d, node n with child logits x_j and
+// probabilities p_j receives, for every child j,
+//   G[n, j] = sum_{u under child j} dl_u  -  p_j * sum_{u under n} dl_u
+// (zero where the logit was clamped).  A query's distinct blocks are sorted,
+// so the blocks under any node are one contiguous run: the first block of the
+// run (the "leader") writes that node's b entries of G, summing in block
+// order -- no conflicts, no atomics.  Then
+//   tree_dq_kernel:   dq = sum_u dq_pair[u] + sum_chunks G C_chunk      (MFMA)
+//   tree_dsum_kernel: dC_chunk = sum_queries G^T Q per query split      (MFMA)
+//   dsum_reduce_kernel adds the splits in order;
+//   pool_adjoint_kernel: dk = dk_leaf + (summaries map)^T dC, which for
+//   compat summaries is the transpose of the reference's Haar keys
+//   (_treeattn_common.py:70-86).
 // The causal correction adds the same -log A_root to every sample of a
 // query; since sum_s dlogp_s = 0 it has no gradient.
 #include "launch.h"
 
 namespace ta {
+
+constexpr int kXS = kChunk + 4;       // padded row stride (floats) of the logit tile
+constexpr int kGS = kChunk + 8;       // padded row stride (elements) of G[q][col]
+constexpr int kGT = kQueryTile + 8;   // padded row stride (elements) of G^T[col][q]
 
 struct TreeArgs {
   Geo geo;
@@ -26,16 +35,14 @@ struct TreeArgs {
   float maxhalf;
   const void* q;
   int64_t qsb, qsl, qsh;
-  const float* weights;
-  int64_t wsb, wsl, wsh;
   const void* sum_hi;  // E (BH, NS, D) (float inputs: the float summaries)
   const void* sum_t;   // E (BH, D, NS)
-  const int* leaf;
   const int* slot_leaf;
   const int* slot_count;
+  const float* slot_weight;
   const float* delta;
   const void* dq_part;
-  float* dlogp;
+  float* dl;           // (B, L, H, S) per distinct block
   void* dq;
   float* dsum_part;
   float* dsum;
@@ -66,49 +73,129 @@ __device__ __forceinline__ void z8(E* o) {
 
 __device__ __forceinline__ float clamp_h(float x, float m) { return fminf(fmaxf(x, -m), m); }
 
-// Raw child logits of level `lam`, columns [c0, c0+ncols), into Xs[64][kChunk].
-template <typename E, int D>
-__device__ __forceinline__ void logits_tile(const E* Qs, float* Xs, const E* sum, int64_t row0, int ncols, int lane,
-                                            int w) {
-  using M = Mfma<E>;
-  const int col = lane & 15, g = lane >> 4;
-  const int ntiles = (ncols + 15) >> 4;
-  for (int nt = 0; nt < ntiles; ++nt) {
-    f32x4 c = zero4();
-    const E* bp = sum + (row0 + nt * 16 + col) * D + M::KPL * g;
-    const E* ap = Qs + (16 * w + col) * D + M::KPL * g;
-#pragma unroll
-    for (int ks = 0; ks < D / M::K; ++ks) c = M::mma(ld_frag(ap + ks * M::K), ld_frag(bp + ks * M::K), c);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[(16 * w + 4 * g + r) * kChunk + nt * 16 + col] = c[r];
-  }
+// dl_u = W_u (delta_u - sum_u' W_u' delta_u').  Lane group of P lanes (P =
+// S rounded up to a power of two) per (b, l, h); butterfly sum in the group.
+__global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__ slot_count,
+                                                         const float* __restrict__ slot_weight,
+                                                         const float* __restrict__ delta, float* __restrict__ dl,
+                                                         int S, int P, int64_t nqh) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t qh = gid / P;
+  const int u = (int)(gid - qh * P);
+  const bool in = qh < nqh;
+  const int n = in ? slot_count[qh] : 0;
+  const bool act = u < n;
+  const float w = act ? slot_weight[qh * S + u] : 0.f;
+  const float dt = act ? delta[qh * S + u] : 0.f;
+  float tot = w * dt;
+  for (int o = 1; o < P; o <<= 1) tot += __shfl_xor(tot, o, 64);
+  if (act) dl[qh * S + u] = w * (dt - tot);
 }
 
-// Adds query qi's dx terms for depth d and chunk [c0, c0+ncols) into
-// G[qi*gq + col*gc].  Samples are visited in order (deterministic).
-__device__ __forceinline__ void build_g_row(const Geo& G, int qi, int d, int c0, int ncols, int S, float maxhalf,
-                                            const float* Xs, const int* lf, const float* dl, float* Gm, int gq,
-                                            int gc) {
-  const int b = G.b, T = G.T;
-  for (int s = 0; s < S; ++s) {
-    const int beta = lf[qi * S + s];
-    const int i = beta / G.pw[T - d];
-    const int base = b * i - c0;
+// Query tile shared by the two tree kernels: the distinct leaf blocks of each
+// query, their dl and count (the Q rows live in registers as MFMA fragments).
+template <typename E, int D>
+struct TileSmem {
+  E* Qt;       // dsum only: [D][kGT] Q transposed
+  float* Xs;   // [64][kXS]
+  E* Gm;       // dq: [64][kGS], dsum: [kChunk][kGT]
+  int* lf;     // [64][S]
+  float* dls;  // [64][S]
+  int* cn;     // [64]
+};
+
+template <typename E, int D>
+__device__ __forceinline__ void load_tile(const TreeArgs& a, const TileSmem<E, D>& sm, RowFrags<E, D>& qf, int bb,
+                                          int h, int l0, int nq, int tid) {
+  const int lane = tid & 63, w = tid >> 6;
+  {
+    const int r = 16 * w + (lane & 15);
+    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
+  }
+  const int S = a.S;
+  const int64_t qh0 = ((int64_t)bb * a.L + l0) * a.H + h;
+  for (int e = tid; e < kQueryTile * S; e += 256) {
+    const int qi = e / S, u = e - qi * S;
+    const int64_t o = (qh0 + (int64_t)qi * a.H) * S + u;
+    sm.lf[e] = qi < nq ? a.slot_leaf[o] : 0;
+    sm.dls[e] = qi < nq ? a.dl[o] : 0.f;
+  }
+  if (tid < kQueryTile) sm.cn[tid] = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
+}
+
+// Next query tile held in registers while the current one computes: its Q
+// fragments, per-query distinct blocks and dl, counts.
+template <typename E, int D, int kSmax>
+struct TileRegs {
+  static constexpr int kItems = kQueryTile * kSmax / 256;
+  RowFrags<E, D> qf;
+  int lf[kItems];
+  float dl[kItems];
+  int cn;
+  __device__ __forceinline__ void load(const TreeArgs& a, int bb, int h, int l0, int nq, int tid) {
+    const int lane = tid & 63, w = tid >> 6;
+    const int r = 16 * w + (lane & 15);
+    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
+    const int S = a.S;
+    const int64_t qh0 = ((int64_t)bb * a.L + l0) * a.H + h;
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const int e = tid + 256 * i;
+      const int qi = e / S, u = e - qi * S;
+      const bool ok = e < kQueryTile * S && qi < nq;
+      const int64_t o = (qh0 + (int64_t)qi * a.H) * S + u;
+      lf[i] = ok ? a.slot_leaf[o] : 0;
+      dl[i] = ok ? a.dl[o] : 0.f;
+    }
+    cn = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
+  }
+  __device__ __forceinline__ void store(int* slf, float* sdl, int* scn, int S, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const int e = tid + 256 * i;
+      if (e < kQueryTile * S) {
+        slf[e] = lf[i];
+        sdl[e] = dl[i];
+      }
+    }
+    if (tid < kQueryTile) scn[tid] = cn;
+  }
+};
+
+// Leader-based G for depth d, chunk [c0, c0+ncols): G[qi*gq + col*gc].
+template <typename E>
+__device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, int S, int nq, float maxhalf,
+                                        const float* Xs, const int* lf, const float* dls, const int* cn, E* Gm,
+                                        int gq, int gc, int tid) {
+  const int b = G.b, lb = G.lb;
+  const int sh = lb * (G.T - d), sh2 = sh - lb;
+  for (int e = tid; e < kQueryTile * S; e += 256) {
+    const int qi = e / S, u = e - qi * S;
+    if (qi >= nq || u >= cn[qi]) continue;
+    const int* L_ = lf + qi * S;
+    const int n = L_[u] >> sh;
+    if (u > 0 && (L_[u - 1] >> sh) == n) continue;
+    const int base = (n << lb) - c0;
     if (base < 0 || base >= ncols) continue;
-    const int js = (beta / G.pw[T - 1 - d]) % b;
-    const float* xr = Xs + qi * kChunk + base;
+    const float* D_ = dls + qi * S;
+    const int cnt = cn[qi];
+    int end = u + 1;
+    float V = D_[u];
+    while (end < cnt && (L_[end] >> sh) == n) V += D_[end++];
+    const float* xr = Xs + qi * kXS + base;
     float mx = -__builtin_inff();
     for (int j = 0; j < b; ++j) mx = fmaxf(mx, clamp_h(xr[j], maxhalf));
     float se = 0.f;
-    for (int j = 0; j < b; ++j) se += expf(clamp_h(xr[j], maxhalf) - mx);
-    const float lse = mx + logf(se);
-    const float dls = dl[qi * S + s];
+    for (int j = 0; j < b; ++j) se += __expf(clamp_h(xr[j], maxhalf) - mx);
+    const float lse = mx + __logf(se);
+    int v = u;
     for (int j = 0; j < b; ++j) {
+      float Vj = 0.f;
+      while (v < end && ((L_[v] >> sh2) & (b - 1)) == j) Vj += D_[v++];
       const float x = xr[j];
       const bool live = x >= -maxhalf && x <= maxhalf;
-      const float p = expf(clamp_h(x, maxhalf) - lse);
-      const float dx = live ? dls * ((j == js ? 1.f : 0.f) - p) : 0.f;
-      Gm[qi * gq + (base + j) * gc] += dx;
+      const float p = __expf(clamp_h(x, maxhalf) - lse);
+      Gm[qi * gq + (base + j) * gc] = (E)(live ? Vj - p * V : 0.f);
     }
   }
 }
@@ -125,42 +212,16 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
   const int64_t rows = G.NS;
 
-  E* Qs = (E*)smem;                                  // [64][D]
-  float* Xs = (float*)(Qs + kQueryTile * D);        // [64][kChunk] (also [64][D] staging)
-  float* Gm = Xs + kQueryTile * kChunk;             // [64][kChunk]
-  int* lf = (int*)(Gm + kQueryTile * kChunk);       // [64*S]
-  float* dl = (float*)(lf + kQueryTile * S);        // [64*S]
+  TileSmem<E, D> sm;
+  sm.Qt = nullptr;
+  sm.Xs = (float*)smem;
+  sm.Gm = (E*)(sm.Xs + kQueryTile * kXS);
+  sm.lf = (int*)(sm.Gm + kQueryTile * kGS);
+  sm.dls = (float*)(sm.lf + kQueryTile * S);
+  sm.cn = (int*)(sm.dls + kQueryTile * S);
 
-  const E* q = (const E*)a.q;
-  for (int e = tid; e < kQueryTile * D / 8; e += 256) {
-    const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
-    if (r < nq) cp8(Qs + r * D + c, q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh + c);
-    else z8(Qs + r * D + c);
-  }
-  // dlogp per sample, one wavefront per query
-  for (int qi = w; qi < kQueryTile; qi += 4) {
-    const bool act = lane < S && qi < nq;
-    const int l = l0 + qi;
-    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    int beta = 0;
-    float wt = 0.f, dlt = 0.f;
-    if (act) {
-      beta = a.leaf[qh * S + lane];
-      wt = a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + lane];
-      const int n = a.slot_count[qh];
-      int u = 0;
-      for (int j = 0; j < n; ++j)
-        if (a.slot_leaf[qh * S + j] == beta) u = j;
-      dlt = a.delta[qh * S + u];
-    }
-    const float tot = wave_sum(wt * dlt);
-    const float dls = wt * (dlt - tot);
-    if (lane < S) {
-      lf[qi * S + lane] = beta;
-      dl[qi * S + lane] = act ? dls : 0.f;
-      if (act) a.dlogp[qh * S + lane] = dls;
-    }
-  }
+  RowFrags<E, D> qf;
+  load_tile<E, D>(a, sm, qf, bb, h, l0, nq, tid);
   __syncthreads();
 
   f32x4 dacc[D / 16];
@@ -172,53 +233,57 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
     const int lam = d + 1, lvl = G.pw[lam];
     for (int c0 = 0; c0 < lvl; c0 += kChunk) {
       const int ncols = min(kChunk, lvl - c0);
-      logits_tile<E, D>(Qs, Xs, sum_hi, (int64_t)bh * rows + G.off[lam] + c0, ncols, lane, w);
-      for (int e = tid; e < kQueryTile * kChunk; e += 256) Gm[e] = 0.f;
+      const int kcols = (ncols + 31) / 32 * 32;
+      const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
+      mfma_rows<E, D, false>(qf, sm.Xs, kXS, sum_hi, nullptr, r0, ncols, r0, lane, w);
+      for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
+        const int r = e / (kcols / 8), c = (e - r * (kcols / 8)) * 8;
+        z8(sm.Gm + r * kGS + c);
+      }
       __syncthreads();
-      if (tid < nq) build_g_row(G, tid, d, c0, ncols, S, a.maxhalf, Xs, lf, dl, Gm, kChunk, 1);
+      build_g<E>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, kGS, 1, tid);
       __syncthreads();
-      const int ksteps = (ncols + M::K - 1) / M::K;
+      const int ksteps = kcols / M::K;
+      const E* ap = sm.Gm + (16 * w + col) * kGS + M::KPL * g;
+      const E* bp = sum_t + ((int64_t)bh * D + col) * rows + G.off[lam] + c0 + M::KPL * g;
+      for (int ks = 0; ks < ksteps; ++ks) {
+        const auto af = ld_frag(ap + ks * M::K);
 #pragma unroll
-      for (int nd = 0; nd < D / 16; ++nd) {
-        const E* bp = sum_t + ((int64_t)bh * D + 16 * nd + col) * rows + G.off[lam] + c0 + M::KPL * g;
-        const float* ap = Gm + (16 * w + col) * kChunk + M::KPL * g;
-        for (int ks = 0; ks < ksteps; ++ks)
-          dacc[nd] = M::mma(cvt_frag<E>(ap + ks * M::K, 1), ld_frag(bp + ks * M::K), dacc[nd]);
+        for (int nd = 0; nd < D / 16; ++nd)
+          dacc[nd] = M::mma(af, ld_frag(bp + (int64_t)16 * nd * rows + ks * M::K), dacc[nd]);
       }
       __syncthreads();
     }
   }
-  // stage tree dq, add the leaf parts, write
-  float* stage = Xs;
+  // stage the tree dq, add the leaf parts, write
+  constexpr int SS = D + 4;
+  float* stage = sm.Xs;  // [64][D+4] fits in [64][kXS]
 #pragma unroll
   for (int nd = 0; nd < D / 16; ++nd)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) stage[(16 * w + 4 * g + r) * D + 16 * nd + col] = dacc[nd][r];
+    for (int r = 0; r < 4; ++r) stage[(16 * w + 4 * g + r) * SS + 16 * nd + col] = dacc[nd][r];
   __syncthreads();
   const E* dqp = (const E*)a.dq_part;
   E* dq = (E*)a.dq;
-  for (int e = tid; e < nq * (D / 4); e += 256) {
-    const int qi = e / (D / 4), d0 = (e - qi * (D / 4)) * 4;
+  for (int e = tid; e < nq * (D / 8); e += 256) {
+    const int qi = e / (D / 8), d0 = (e - qi * (D / 8)) * 8;
     const int l = l0 + qi;
     const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    float acc[4];
+    float acc[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = stage[qi * D + d0 + i];
-    const int n = a.slot_count[qh];
-    for (int u = 0; u < n; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += tof(dqp[(qh * S + u) * D + d0 + i]);
+    for (int i = 0; i < 8; ++i) acc[i] = stage[qi * SS + d0 + i];
+    sum_rows8(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
     E* o = dq + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + d0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (E)acc[i];
+    for (int i = 0; i < 8; ++i) o[i] = (E)acc[i];
   }
 }
 
-// grid (ncol, BH, qsplit).  Column chunk -> (level, c0).
-template <typename E, int D>
+// grid (ncol, BH, qsplit).  Column chunk -> (level, c0).  kSmax bounds S.
+template <typename E, int D, int kSmax>
 __global__ __launch_bounds__(256) void tree_dsum_kernel(TreeArgs a) {
   using M = Mfma<E>;
-  constexpr int NT = (kChunk / 16) * (D / 16) / 4;
+  constexpr int NT = (kDsumChunk / 16) * (D / 16) / 4;
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
@@ -229,18 +294,20 @@ __global__ __launch_bounds__(256) void tree_dsum_kernel(TreeArgs a) {
 
   int lam = 1, c0 = 0, rem = blockIdx.x;
   for (; lam <= T; ++lam) {
-    const int nc = (G.pw[lam] + kChunk - 1) / kChunk;
-    if (rem < nc) { c0 = rem * kChunk; break; }
+    const int nc = (G.pw[lam] + kDsumChunk - 1) / kDsumChunk;
+    if (rem < nc) { c0 = rem * kDsumChunk; break; }
     rem -= nc;
   }
   const int d = lam - 1;
-  const int ncols = min(kChunk, G.pw[lam] - c0);
+  const int ncols = min(kDsumChunk, G.pw[lam] - c0);
 
-  E* Qs = (E*)smem;                              // [64][D]
-  float* Xs = (float*)(Qs + kQueryTile * D);    // [64][kChunk]
-  float* Gt = Xs + kQueryTile * kChunk;         // [kChunk][64]
-  int* lf = (int*)(Gt + kQueryTile * kChunk);   // [64*S]
-  float* dl = (float*)(lf + kQueryTile * S);    // [64*S]
+  TileSmem<E, D> sm;
+  sm.Qt = (E*)smem;
+  sm.Xs = (float*)(sm.Qt + D * kGT);
+  sm.Gm = (E*)(sm.Xs + kQueryTile * kXS);
+  sm.lf = (int*)(sm.Gm + kDsumChunk * kGT);
+  sm.dls = (float*)(sm.lf + kQueryTile * S);
+  sm.cn = (int*)(sm.dls + kQueryTile * S);
 
   f32x4 acc[NT];
 #pragma unroll
@@ -249,44 +316,48 @@ __global__ __launch_bounds__(256) void tree_dsum_kernel(TreeArgs a) {
   const int ntiles = (a.L + kQueryTile - 1) / kQueryTile;
   const int per = (ntiles + a.qsplit - 1) / a.qsplit;
   const int tt0 = split * per, tt1 = min(ntiles, tt0 + per);
-  const E* q = (const E*)a.q;
   const E* sum_hi = (const E*)a.sum_hi;
+  TileRegs<E, D, kSmax> nxt;
+  if (tt0 < tt1) nxt.load(a, bb, h, tt0 * kQueryTile, min(kQueryTile, a.L - tt0 * kQueryTile), tid);
   for (int tt = tt0; tt < tt1; ++tt) {
     const int l0 = tt * kQueryTile;
     const int nq = min(kQueryTile, a.L - l0);
     __syncthreads();
-    for (int e = tid; e < kQueryTile * D / 8; e += 256) {
-      const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
-      if (r < nq) cp8(Qs + r * D + c, q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh + c);
-      else z8(Qs + r * D + c);
+    nxt.store(sm.lf, sm.dls, sm.cn, S, tid);
+    const RowFrags<E, D> qf = nxt.qf;
+    if (tt + 1 < tt1) {
+      const int l1 = l0 + kQueryTile;
+      nxt.load(a, bb, h, l1, min(kQueryTile, a.L - l1), tid);
     }
-    for (int e = tid; e < kQueryTile * S; e += 256) {
-      const int qi = e / S, s = e - qi * S;
-      if (qi < nq) {
-        const int64_t qh = ((int64_t)bb * a.L + l0 + qi) * a.H + h;
-        lf[e] = a.leaf[qh * S + s];
-        dl[e] = a.dlogp[qh * S + s];
+    // Q^T for the G^T Q product: lane holds row 16w+col, dims ks*K + KPL*g + i
+#pragma unroll
+    for (int ks = 0; ks < D / M::K; ++ks) {
+      if constexpr (M::KPL == 1) {
+        sm.Qt[(ks * M::K + g) * kGT + 16 * w + col] = qf.f[ks];
       } else {
-        lf[e] = 0;
-        dl[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < M::KPL; ++i) sm.Qt[(ks * M::K + M::KPL * g + i) * kGT + 16 * w + col] = qf.f[ks][i];
       }
     }
-    for (int e = tid; e < kQueryTile * kChunk; e += 256) Gt[e] = 0.f;
+    for (int e = tid; e < kDsumChunk * kQueryTile / 8; e += 256) {
+      const int r = e / (kQueryTile / 8), c = (e - r * (kQueryTile / 8)) * 8;
+      z8(sm.Gm + r * kGT + c);
+    }
+    const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
+    mfma_rows<E, D, false>(qf, sm.Xs, kXS, sum_hi, nullptr, r0, ncols, r0, lane, w);
     __syncthreads();
-    logits_tile<E, D>(Qs, Xs, sum_hi, (int64_t)bh * rows + G.off[lam] + c0, ncols, lane, w);
-    __syncthreads();
-    if (tid < nq) build_g_row(G, tid, d, c0, ncols, S, a.maxhalf, Xs, lf, dl, Gt, 1, kQueryTile);
+    build_g<E>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, 1, kGT, tid);
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int tile = w + 4 * t;
       const int mc = tile / (D / 16), nd = tile - mc * (D / 16);
       if (16 * mc >= ncols) continue;
-      const float* ap = Gt + (16 * mc + col) * kQueryTile + M::KPL * g;
-      const E* bp = Qs + (M::KPL * g) * D + 16 * nd + col;
+      const E* ap = sm.Gm + (16 * mc + col) * kGT + M::KPL * g;
+      const E* bp = sm.Qt + (16 * nd + col) * kGT + M::KPL * g;
 #pragma unroll
       for (int ks = 0; ks < kQueryTile / M::K; ++ks)
-        acc[t] = M::mma(cvt_frag<E>(ap + ks * M::K, 1), ld_frag_strided(bp + ks * M::K * D, D), acc[t]);
+        acc[t] = M::mma(ld_frag(ap + ks * M::K), ld_frag(bp + ks * M::K), acc[t]);
     }
   }
   float* out = a.dsum_part + ((int64_t)split * gridDim.y + bh) * rows * D;
@@ -317,21 +388,24 @@ __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restric
 }
 
 // dk[b, t, h, :] = dk_leaf + sum over the summaries that include token t.
+// One thread per (token, 4 dims); grid (ceil(N*D/4/256), BH).
 template <typename E>
 __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
   const Geo& G = a.geo;
   const int D = a.D;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)a.N * D) return;
+  if (e >= (int64_t)a.N * D / 4) return;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
-  const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
+  const int t = (int)(e / (D / 4)), d0 = (int)(e - (int64_t)t * (D / 4)) * 4;
   const int beta = t / G.LB;
-  const float* ds = a.dsum + (int64_t)bh * G.NS * D + d;
-  float acc = 0.f;
+  const float* ds = a.dsum + (int64_t)bh * G.NS * D + d0;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (a.mode == TA_TREE_NATURAL) {
     for (int lam = 1; lam <= G.T; ++lam) {
-      const int per = G.NL / G.pw[lam];
-      acc += ds[(int64_t)(G.off[lam] + beta / per) * D] / (2.f * (float)per);
+      const int shift = G.lb * (G.T - lam);  // leaf blocks per node = 2^shift
+      const float4 v = *(const float4*)(ds + (int64_t)(G.off[lam] + (beta >> shift)) * D);
+      const float s = 1.f / (float)(2 << shift);
+      acc[0] += v.x * s; acc[1] += v.y * s; acc[2] += v.z * s; acc[3] += v.w * s;
     }
   } else {
     // compat: dcoef_n = (dC_left - dC_right)/2 for heap node n; the in-order
@@ -343,15 +417,19 @@ __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
       const int dep = 31 - __clz(nn + 1);
       const int ip = nn + 1 - (1 << dep);
       const int64_t rl = G.off[dep + 1] + 2 * ip;
-      const float dcoef = 0.5f * (ds[rl * D] - ds[(rl + 1) * D]);
-      const float term = dcoef / (2.f * (float)wl);
-      acc += beta < p ? term : -term;
+      const float4 x = *(const float4*)(ds + rl * D), y = *(const float4*)(ds + (rl + 1) * D);
+      const float s = (beta < p ? 0.25f : -0.25f) / (float)wl;
+      acc[0] += (x.x - y.x) * s; acc[1] += (x.y - y.y) * s; acc[2] += (x.z - y.z) * s; acc[3] += (x.w - y.w) * s;
     }
   }
-  acc /= (float)G.LB;
+  const float inv = 1.f / (float)G.LB;
   const int64_t th = ((int64_t)bb * a.N + t) * a.H + h;
-  acc += a.dk_leaf[th * D + d];
-  ((E*)a.dk)[bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d] = (E)acc;
+  const float4 lk = *(const float4*)(a.dk_leaf + th * D + d0);
+  E* o = (E*)a.dk + bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d0;
+  o[0] = (E)(lk.x + acc[0] * inv);
+  o[1] = (E)(lk.y + acc[1] * inv);
+  o[2] = (E)(lk.z + acc[2] * inv);
+  o[3] = (E)(lk.w + acc[3] * inv);
 }
 
 // Node-keys mode: dk[node n] = (dC_left - dC_right) / 2.
@@ -371,13 +449,15 @@ __global__ __launch_bounds__(256) void nodekeys_adjoint_kernel(TreeArgs a) {
   ((E*)a.dk)[bb * a.ksb + (int64_t)nn * a.ksl + h * a.ksh + d] = (E)(0.5f * (ds[rl * D] - ds[(rl + 1) * D]));
 }
 
-int tree_dq_smem(const Plan& P) {
-  return kQueryTile * (int)P.D * P.esize + 2 * kQueryTile * kChunk * 4 + kQueryTile * (int)P.S * 8;
+static int tree_smem(const Plan& P, bool dsum) {
+  const int D = (int)P.D, S = (int)P.S;
+  const int g = dsum ? kDsumChunk * kGT + D * kGT : kQueryTile * kGS;
+  return kQueryTile * kXS * 4 + g * P.esize + kQueryTile * S * 8 + kQueryTile * 4;
 }
 
 template <typename E, int D>
-static hipError_t tree_impl(const Plan& P, const void* q, const float* weights, const char* rec, void* dq, void* dk,
-                            char* ws, hipStream_t st) {
+static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void* dq, void* dk, char* ws,
+                            hipStream_t st) {
   TreeArgs a;
   a.geo = P.geo;
   a.L = (int)P.L;
@@ -390,16 +470,14 @@ static hipError_t tree_impl(const Plan& P, const void* q, const float* weights, 
   a.maxhalf = 0.5f * P.p.max_logit;
   a.q = q;
   a.qsb = P.p.q_strides[0]; a.qsl = P.p.q_strides[1]; a.qsh = P.p.q_strides[2];
-  a.weights = weights;
-  a.wsb = P.p.w_strides[0]; a.wsl = P.p.w_strides[1]; a.wsh = P.p.w_strides[2];
   a.sum_hi = sizeof(E) == 2 ? (const void*)(rec + P.rec.sum_hi) : (const void*)(rec + P.rec.summaries);
   a.sum_t = rec + P.rec.sum_t;
-  a.leaf = (const int*)(rec + P.rec.leaf);
   a.slot_leaf = (const int*)(rec + P.rec.slot_leaf);
   a.slot_count = (const int*)(rec + P.rec.slot_count);
+  a.slot_weight = (const float*)(rec + P.rec.slot_weight);
   a.delta = (const float*)(ws + P.bws.delta);
   a.dq_part = ws + P.bws.dq_part;
-  a.dlogp = (float*)(ws + P.bws.dlogp);
+  a.dl = (float*)(ws + P.bws.dlogp);
   a.dq = dq;
   a.dsum_part = (float*)(ws + P.bws.dsum_part);
   a.dsum = (float*)(ws + P.bws.dsum);
@@ -408,15 +486,24 @@ static hipError_t tree_impl(const Plan& P, const void* q, const float* weights, 
   a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
   a.qsplit = P.qsplit;
 
-  const int smem = tree_dq_smem(P);
-  hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  const int64_t nqh = P.B * P.L * P.H;
+  int pw2 = 1;
+  while (pw2 < P.S) pw2 <<= 1;
+  hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
+                     a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh);
+  const int smem_q = tree_smem(P, false), smem_s = tree_smem(P, true);
+  hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
   if (e != hipSuccess) return e;
-  e = hipFuncSetAttribute((const void*)tree_dsum_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  const void* dsum_fn = P.S <= 16 ? (const void*)tree_dsum_kernel<E, D, 16> : (const void*)tree_dsum_kernel<E, D, 64>;
+  e = hipFuncSetAttribute(dsum_fn, hipFuncAttributeMaxDynamicSharedMemorySize, smem_s);
   if (e != hipSuccess) return e;
   const unsigned qtiles = (unsigned)((P.L + kQueryTile - 1) / kQueryTile);
-  hipLaunchKernelGGL((tree_dq_kernel<E, D>), dim3(qtiles, P.BH), dim3(256), smem, st, a);
+  hipLaunchKernelGGL((tree_dq_kernel<E, D>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
   if (P.geo.T > 0) {
-    hipLaunchKernelGGL((tree_dsum_kernel<E, D>), dim3(P.ncol, P.BH, P.qsplit), dim3(256), smem, st, a);
+    if (P.S <= 16)
+      hipLaunchKernelGGL((tree_dsum_kernel<E, D, 16>), dim3(P.ncol, P.BH, P.qsplit), dim3(256), smem_s, st, a);
+    else
+      hipLaunchKernelGGL((tree_dsum_kernel<E, D, 64>), dim3(P.ncol, P.BH, P.qsplit), dim3(256), smem_s, st, a);
     const int64_t n = P.BH * (int64_t)P.geo.NS * D;
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D);
@@ -426,29 +513,29 @@ static hipError_t tree_impl(const Plan& P, const void* q, const float* weights, 
     if (n > 0)
       hipLaunchKernelGGL(nodekeys_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
   } else {
-    const int64_t n = P.N * D;
+    const int64_t n = P.N * D / 4;
     hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
   }
   return hipGetLastError();
 }
 
 template <typename E>
-static hipError_t tree_d(const Plan& P, const void* q, const float* w, const char* rec, void* dq, void* dk, char* ws,
-                         hipStream_t st) {
+static hipError_t tree_d(const Plan& P, const void* q, const char* rec, void* dq, void* dk, char* ws, hipStream_t st) {
   switch (P.D) {
-    case 32: return tree_impl<E, 32>(P, q, w, rec, dq, dk, ws, st);
-    case 64: return tree_impl<E, 64>(P, q, w, rec, dq, dk, ws, st);
-    case 96: return tree_impl<E, 96>(P, q, w, rec, dq, dk, ws, st);
-    default: return tree_impl<E, 128>(P, q, w, rec, dq, dk, ws, st);
+    case 32: return tree_impl<E, 32>(P, q, rec, dq, dk, ws, st);
+    case 64: return tree_impl<E, 64>(P, q, rec, dq, dk, ws, st);
+    case 96: return tree_impl<E, 96>(P, q, rec, dq, dk, ws, st);
+    default: return tree_impl<E, 128>(P, q, rec, dq, dk, ws, st);
   }
 }
 
 hipError_t launch_tree_bwd(const Plan& P, const void* q, const float* weights, const char* rec, void* dq, void* dk,
                            char* ws, hipStream_t st) {
+  (void)weights;  // the record's summed weight per distinct leaf block carries what the backward needs
   switch (P.p.dtype) {
-    case TA_F32: return tree_d<float>(P, q, weights, rec, dq, dk, ws, st);
-    case TA_BF16: return tree_d<bf16>(P, q, weights, rec, dq, dk, ws, st);
-    default: return tree_d<f16>(P, q, weights, rec, dq, dk, ws, st);
+    case TA_F32: return tree_d<float>(P, q, rec, dq, dk, ws, st);
+    case TA_BF16: return tree_d<bf16>(P, q, rec, dq, dk, ws, st);
+    default: return tree_d<f16>(P, q, rec, dq, dk, ws, st);
   }
 }
 
