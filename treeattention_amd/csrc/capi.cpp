@@ -107,14 +107,15 @@ int make_plan(const ta_problem* p, Plan* P) {
   if ((int64_t)NL * P->nchunk * P->BH > ((int64_t)1 << 29))
     return fail(TA_ERR_UNSUPPORTED, "too many leaf blocks x query chunks for the bucket table (NL=%lld)",
                 (long long)NL);
-  int ncol = 0;
-  for (int lam = 1; lam <= T; ++lam) ncol += (G.pw[lam] + kDsumChunk - 1) / kDsumChunk;
-  P->ncol = ncol;
-  const int qtiles = (int)((L + kQueryTile - 1) / kQueryTile);
-  int qsplit = ncol > 0 ? (int)((2048 + ncol * P->BH - 1) / (ncol * P->BH)) : 1;
+  // summary gradient: 64-row tiles of the summaries, queries split so the
+  // product has a few thousand workgroups
+  const int64_t qtiles = (L + kQueryTile - 1) / kQueryTile;
+  P->Lp = qtiles * kQueryTile;
+  const int64_t rowtiles = (G.NS + 63) / 64;
+  int64_t qsplit = rowtiles > 0 ? (4096 + rowtiles * P->BH - 1) / (rowtiles * P->BH) : 1;
   if (qsplit < 1) qsplit = 1;
   if (qsplit > qtiles) qsplit = qtiles;
-  P->qsplit = qsplit;
+  P->qsplit = (int)qsplit;
 
   const int64_t BLHS = B * L * H * S;
   const int64_t es = P->esize;
@@ -141,7 +142,9 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->bws.dq_part = w.take(BLHS * D * es);
   P->bws.dlogp = w.take(BLHS * 4);
   P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : B * N * H * D * 4);
-  P->bws.dsum_part = w.take((int64_t)qsplit * P->BH * G.NS * D * 4);
+  P->bws.gt = w.take(P->BH * G.NS * P->Lp * es);
+  P->bws.qt = w.take(P->BH * D * P->Lp * es);
+  P->bws.dsum_part = w.take(qsplit * P->BH * G.NS * D * 4);
   P->bws.dsum = w.take(P->BH * G.NS * D * 4);
   P->bws.total = w.at;
 

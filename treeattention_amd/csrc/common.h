@@ -20,7 +20,6 @@ constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 cov
 constexpr int kMaxSamples = 64;   // one wavefront lane per sample
 constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
 constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
-constexpr int kDsumChunk = 64;    // summary columns per workgroup of the summary-gradient kernel
 
 // Tree geometry.  Child summaries are stored level-major: level lam (1..T)
 // holds b^lam rows starting at off[lam], padded with zero rows to a multiple
@@ -346,6 +345,8 @@ struct BwdWorkspaceLayout {
   int64_t dq_part;   // E (B, L, H, S, D): leaf dq per distinct leaf block
   int64_t dlogp;     // float (B, L, H, S): gradient of each distinct leaf block's summed log-prob
   int64_t dk_leaf;   // float (B, N, H, D)
+  int64_t gt;        // E (BH, NS, Lp): gradient of the child logits, transposed (queries contiguous)
+  int64_t qt;        // E (BH, D, Lp): queries transposed
   int64_t dsum_part; // float (qsplit, BH, NS, D)
   int64_t dsum;      // float (BH, NS, D)
   int64_t total;

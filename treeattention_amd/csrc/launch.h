@@ -13,8 +13,8 @@ struct Plan {
   int esize;        // bytes per element of q/k/v
   int qc;           // queries per bucketing chunk
   int nchunk;       // bucketing chunks per (batch, head)
-  int ncol;         // child-summary chunks of kDsumChunk columns over all levels
-  int qsplit;       // query splits of the summary-gradient kernel
+  int64_t Lp;       // L rounded up to a multiple of kQueryTile
+  int qsplit;       // query splits of the summary-gradient product
   RecordLayout rec;
   FwdWorkspaceLayout fws;
   BwdWorkspaceLayout bws;

@@ -13,8 +13,10 @@
 // so the blocks under any node are one contiguous run: the first block of the
 // run (the "leader") writes that node's b entries of G, summing in block
 // order -- no conflicts, no atomics.  Then
-//   tree_dq_kernel:   dq = sum_u dq_pair[u] + sum_chunks G C_chunk      (MFMA)
-//   tree_dsum_kernel: dC_chunk = sum_queries G^T Q per query split      (MFMA)
+//   tree_dq_kernel: dq = sum_u dq_pair[u] + sum_chunks G C_chunk (MFMA); it
+//     also writes G^T and Q^T with the queries contiguous;
+//   tree_dc_kernel: dC = G^T Q per query split, a plain MFMA product of the
+//     two (no recomputation of logits or G);
 //   dsum_reduce_kernel adds the splits in order;
 //   pool_adjoint_kernel: dk = dk_leaf + (summaries map)^T dC, which for
 //   compat summaries is the transpose of the reference's Haar keys
@@ -27,7 +29,6 @@ namespace ta {
 
 constexpr int kXS = kChunk + 4;       // padded row stride (floats) of the logit tile
 constexpr int kGS = kChunk + 8;       // padded row stride (elements) of G[q][col]
-constexpr int kGT = kQueryTile + 8;   // padded row stride (elements) of G^T[col][q]
 
 struct TreeArgs {
   Geo geo;
@@ -43,6 +44,9 @@ struct TreeArgs {
   const float* delta;
   const void* dq_part;
   float* dl;           // (B, L, H, S) per distinct block
+  void* gt;            // E (BH, NS, Lp)
+  void* qt;            // E (BH, D, Lp)
+  int64_t Lp;
   void* dq;
   float* dsum_part;
   float* dsum;
@@ -92,13 +96,12 @@ __global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__
   if (act) dl[qh * S + u] = w * (dt - tot);
 }
 
-// Query tile shared by the two tree kernels: the distinct leaf blocks of each
-// query, their dl and count (the Q rows live in registers as MFMA fragments).
+// Query tile of the dq kernel: the distinct leaf blocks of each query, their
+// dl and count (the Q rows live in registers as MFMA fragments).
 template <typename E, int D>
 struct TileSmem {
-  E* Qt;       // dsum only: [D][kGT] Q transposed
   float* Xs;   // [64][kXS]
-  E* Gm;       // dq: [64][kGS], dsum: [kChunk][kGT]
+  E* Gm;       // [64][kGS]
   int* lf;     // [64][S]
   float* dls;  // [64][S]
   int* cn;     // [64]
@@ -122,45 +125,6 @@ __device__ __forceinline__ void load_tile(const TreeArgs& a, const TileSmem<E, D
   }
   if (tid < kQueryTile) sm.cn[tid] = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
 }
-
-// Next query tile held in registers while the current one computes: its Q
-// fragments, per-query distinct blocks and dl, counts.
-template <typename E, int D, int kSmax>
-struct TileRegs {
-  static constexpr int kItems = kQueryTile * kSmax / 256;
-  RowFrags<E, D> qf;
-  int lf[kItems];
-  float dl[kItems];
-  int cn;
-  __device__ __forceinline__ void load(const TreeArgs& a, int bb, int h, int l0, int nq, int tid) {
-    const int lane = tid & 63, w = tid >> 6;
-    const int r = 16 * w + (lane & 15);
-    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
-    const int S = a.S;
-    const int64_t qh0 = ((int64_t)bb * a.L + l0) * a.H + h;
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const int e = tid + 256 * i;
-      const int qi = e / S, u = e - qi * S;
-      const bool ok = e < kQueryTile * S && qi < nq;
-      const int64_t o = (qh0 + (int64_t)qi * a.H) * S + u;
-      lf[i] = ok ? a.slot_leaf[o] : 0;
-      dl[i] = ok ? a.dl[o] : 0.f;
-    }
-    cn = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
-  }
-  __device__ __forceinline__ void store(int* slf, float* sdl, int* scn, int S, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const int e = tid + 256 * i;
-      if (e < kQueryTile * S) {
-        slf[e] = lf[i];
-        sdl[e] = dl[i];
-      }
-    }
-    if (tid < kQueryTile) scn[tid] = cn;
-  }
-};
 
 // Leader-based G for depth d, chunk [c0, c0+ncols): G[qi*gq + col*gc].
 template <typename E>
@@ -213,7 +177,6 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
   const int64_t rows = G.NS;
 
   TileSmem<E, D> sm;
-  sm.Qt = nullptr;
   sm.Xs = (float*)smem;
   sm.Gm = (E*)(sm.Xs + kQueryTile * kXS);
   sm.lf = (int*)(sm.Gm + kQueryTile * kGS);
@@ -222,6 +185,19 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
 
   RowFrags<E, D> qf;
   load_tile<E, D>(a, sm, qf, bb, h, l0, nq, tid);
+  {
+    // Q^T for the summary-gradient product (rows past nq are zero fragments)
+    E* qt = (E*)a.qt + (int64_t)bh * D * a.Lp + l0 + 16 * w + col;
+#pragma unroll
+    for (int ks = 0; ks < D / M::K; ++ks) {
+      if constexpr (M::KPL == 1) {
+        qt[(int64_t)(ks * M::K + g) * a.Lp] = qf.f[ks];
+      } else {
+#pragma unroll
+        for (int i = 0; i < M::KPL; ++i) qt[(int64_t)(ks * M::K + M::KPL * g + i) * a.Lp] = qf.f[ks][i];
+      }
+    }
+  }
   __syncthreads();
 
   f32x4 dacc[D / 16];
@@ -243,6 +219,18 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
       __syncthreads();
       build_g<E>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, kGS, 1, tid);
       __syncthreads();
+      {
+        // G^T rows of the chunk (kcols covers the level's zero padding rows),
+        // eight queries per 16-byte store
+        E* gt = (E*)a.gt + ((int64_t)bh * rows + G.off[lam] + c0) * a.Lp + l0;
+        for (int e = tid; e < kcols * (kQueryTile / 8); e += 256) {
+          const int c = e >> 3, q0 = (e & 7) * 8;
+          E v8[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v8[i] = sm.Gm[(q0 + i) * kGS + c];
+          cp8(gt + (int64_t)c * a.Lp + q0, v8);
+        }
+      }
       const int ksteps = kcols / M::K;
       const E* ap = sm.Gm + (16 * w + col) * kGS + M::KPL * g;
       const E* bp = sum_t + ((int64_t)bh * D + col) * rows + G.off[lam] + c0 + M::KPL * g;
@@ -279,98 +267,53 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
   }
 }
 
-// grid (ncol, BH, qsplit).  Column chunk -> (level, c0).  kSmax bounds S.
-template <typename E, int D, int kSmax>
-__global__ __launch_bounds__(256) void tree_dsum_kernel(TreeArgs a) {
+// dC partial of one query split: dsum_part[split][bh][r][:] = sum over the
+// split's queries of G^T[r][q] Q[q][:].  Both operands are stored with the
+// queries contiguous, so every fragment is one contiguous load from global
+// memory.  grid (ceil(NS/64), BH, qsplit); wave w owns rows 16w..16w+15 of
+// the workgroup's 64 (NS is a multiple of 32, so a wave is in or out whole).
+template <typename E, int D>
+__global__ __launch_bounds__(256) void tree_dc_kernel(TreeArgs a) {
   using M = Mfma<E>;
-  constexpr int NT = (kDsumChunk / 16) * (D / 16) / 4;
-  extern __shared__ __align__(16) char smem[];
-  const Geo& G = a.geo;
-  const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
-  const int split = blockIdx.z;
-  const int S = a.S, T = G.T;
+  using F = typename M::frag;
+  const int bh = blockIdx.y, split = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
-  const int64_t rows = G.NS;
+  const int rows = a.geo.NS;
+  const int r0 = 64 * blockIdx.x + 16 * w;
+  if (r0 >= rows) return;
+  const int64_t Lp = a.Lp;
+  const int64_t per = ((Lp / kQueryTile + a.qsplit - 1) / a.qsplit) * kQueryTile;
+  const int64_t k0 = (int64_t)split * per, k1 = min(Lp, k0 + per);
+  const E* ap = (const E*)a.gt + ((int64_t)bh * rows + r0 + col) * Lp + M::KPL * g;
+  const E* bp = (const E*)a.qt + ((int64_t)bh * D + col) * Lp + M::KPL * g;
 
-  int lam = 1, c0 = 0, rem = blockIdx.x;
-  for (; lam <= T; ++lam) {
-    const int nc = (G.pw[lam] + kDsumChunk - 1) / kDsumChunk;
-    if (rem < nc) { c0 = rem * kDsumChunk; break; }
-    rem -= nc;
-  }
-  const int d = lam - 1;
-  const int ncols = min(kDsumChunk, G.pw[lam] - c0);
-
-  TileSmem<E, D> sm;
-  sm.Qt = (E*)smem;
-  sm.Xs = (float*)(sm.Qt + D * kGT);
-  sm.Gm = (E*)(sm.Xs + kQueryTile * kXS);
-  sm.lf = (int*)(sm.Gm + kDsumChunk * kGT);
-  sm.dls = (float*)(sm.lf + kQueryTile * S);
-  sm.cn = (int*)(sm.dls + kQueryTile * S);
-
-  f32x4 acc[NT];
+  f32x4 acc[D / 16];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = zero4();
-
-  const int ntiles = (a.L + kQueryTile - 1) / kQueryTile;
-  const int per = (ntiles + a.qsplit - 1) / a.qsplit;
-  const int tt0 = split * per, tt1 = min(ntiles, tt0 + per);
-  const E* sum_hi = (const E*)a.sum_hi;
-  TileRegs<E, D, kSmax> nxt;
-  if (tt0 < tt1) nxt.load(a, bb, h, tt0 * kQueryTile, min(kQueryTile, a.L - tt0 * kQueryTile), tid);
-  for (int tt = tt0; tt < tt1; ++tt) {
-    const int l0 = tt * kQueryTile;
-    const int nq = min(kQueryTile, a.L - l0);
-    __syncthreads();
-    nxt.store(sm.lf, sm.dls, sm.cn, S, tid);
-    const RowFrags<E, D> qf = nxt.qf;
-    if (tt + 1 < tt1) {
-      const int l1 = l0 + kQueryTile;
-      nxt.load(a, bb, h, l1, min(kQueryTile, a.L - l1), tid);
-    }
-    // Q^T for the G^T Q product: lane holds row 16w+col, dims ks*K + KPL*g + i
+  for (int nd = 0; nd < D / 16; ++nd) acc[nd] = zero4();
+  if (k0 < k1) {
+    F af = ld_frag(ap + k0);
+    F bf[D / 16];
 #pragma unroll
-    for (int ks = 0; ks < D / M::K; ++ks) {
-      if constexpr (M::KPL == 1) {
-        sm.Qt[(ks * M::K + g) * kGT + 16 * w + col] = qf.f[ks];
-      } else {
+    for (int nd = 0; nd < D / 16; ++nd) bf[nd] = ld_frag(bp + (int64_t)16 * nd * Lp + k0);
+    for (int64_t k = k0; k < k1; k += M::K) {
+      const F ac = af;
+      F bc[D / 16];
 #pragma unroll
-        for (int i = 0; i < M::KPL; ++i) sm.Qt[(ks * M::K + M::KPL * g + i) * kGT + 16 * w + col] = qf.f[ks][i];
+      for (int nd = 0; nd < D / 16; ++nd) bc[nd] = bf[nd];
+      if (k + M::K < k1) {
+        af = ld_frag(ap + k + M::K);
+#pragma unroll
+        for (int nd = 0; nd < D / 16; ++nd) bf[nd] = ld_frag(bp + (int64_t)16 * nd * Lp + k + M::K);
       }
-    }
-    for (int e = tid; e < kDsumChunk * kQueryTile / 8; e += 256) {
-      const int r = e / (kQueryTile / 8), c = (e - r * (kQueryTile / 8)) * 8;
-      z8(sm.Gm + r * kGT + c);
-    }
-    const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
-    mfma_rows<E, D, false>(qf, sm.Xs, kXS, sum_hi, nullptr, r0, ncols, r0, lane, w);
-    __syncthreads();
-    build_g<E>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, 1, kGT, tid);
-    __syncthreads();
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tile = w + 4 * t;
-      const int mc = tile / (D / 16), nd = tile - mc * (D / 16);
-      if (16 * mc >= ncols) continue;
-      const E* ap = sm.Gm + (16 * mc + col) * kGT + M::KPL * g;
-      const E* bp = sm.Qt + (16 * nd + col) * kGT + M::KPL * g;
-#pragma unroll
-      for (int ks = 0; ks < kQueryTile / M::K; ++ks)
-        acc[t] = M::mma(ld_frag(ap + ks * M::K), ld_frag(bp + ks * M::K), acc[t]);
+      for (int nd = 0; nd < D / 16; ++nd) acc[nd] = M::mma(ac, bc[nd], acc[nd]);
     }
   }
   float* out = a.dsum_part + ((int64_t)split * gridDim.y + bh) * rows * D;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int tile = w + 4 * t;
-    const int mc = tile / (D / 16), nd = tile - mc * (D / 16);
+  for (int nd = 0; nd < D / 16; ++nd)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = 16 * mc + 4 * g + r;
-      if (c < ncols) out[(int64_t)(G.off[lam] + c0 + c) * D + 16 * nd + col] = acc[t][r];
-    }
-  }
+    for (int r = 0; r < 4; ++r) out[(int64_t)(r0 + 4 * g + r) * D + 16 * nd + col] = acc[nd][r];
 }
 
 // dsum = sum over query splits (in split order); rows outside any level are 0.
@@ -449,10 +392,9 @@ __global__ __launch_bounds__(256) void nodekeys_adjoint_kernel(TreeArgs a) {
   ((E*)a.dk)[bb * a.ksb + (int64_t)nn * a.ksl + h * a.ksh + d] = (E)(0.5f * (ds[rl * D] - ds[(rl + 1) * D]));
 }
 
-static int tree_smem(const Plan& P, bool dsum) {
-  const int D = (int)P.D, S = (int)P.S;
-  const int g = dsum ? kDsumChunk * kGT + D * kGT : kQueryTile * kGS;
-  return kQueryTile * kXS * 4 + g * P.esize + kQueryTile * S * 8 + kQueryTile * 4;
+static int tree_smem(const Plan& P) {
+  const int S = (int)P.S;
+  return kQueryTile * kXS * 4 + kQueryTile * kGS * P.esize + kQueryTile * S * 8 + kQueryTile * 4;
 }
 
 template <typename E, int D>
@@ -478,6 +420,9 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.delta = (const float*)(ws + P.bws.delta);
   a.dq_part = ws + P.bws.dq_part;
   a.dl = (float*)(ws + P.bws.dlogp);
+  a.gt = ws + P.bws.gt;
+  a.qt = ws + P.bws.qt;
+  a.Lp = P.Lp;
   a.dq = dq;
   a.dsum_part = (float*)(ws + P.bws.dsum_part);
   a.dsum = (float*)(ws + P.bws.dsum);
@@ -491,19 +436,14 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   while (pw2 < P.S) pw2 <<= 1;
   hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
                      a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh);
-  const int smem_q = tree_smem(P, false), smem_s = tree_smem(P, true);
+  const int smem_q = tree_smem(P);
   hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
   if (e != hipSuccess) return e;
-  const void* dsum_fn = P.S <= 16 ? (const void*)tree_dsum_kernel<E, D, 16> : (const void*)tree_dsum_kernel<E, D, 64>;
-  e = hipFuncSetAttribute(dsum_fn, hipFuncAttributeMaxDynamicSharedMemorySize, smem_s);
-  if (e != hipSuccess) return e;
-  const unsigned qtiles = (unsigned)((P.L + kQueryTile - 1) / kQueryTile);
+  const unsigned qtiles = (unsigned)(P.Lp / kQueryTile);
   hipLaunchKernelGGL((tree_dq_kernel<E, D>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
   if (P.geo.T > 0) {
-    if (P.S <= 16)
-      hipLaunchKernelGGL((tree_dsum_kernel<E, D, 16>), dim3(P.ncol, P.BH, P.qsplit), dim3(256), smem_s, st, a);
-    else
-      hipLaunchKernelGGL((tree_dsum_kernel<E, D, 64>), dim3(P.ncol, P.BH, P.qsplit), dim3(256), smem_s, st, a);
+    const unsigned rowtiles = (unsigned)((P.geo.NS + 63) / 64);
+    hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(rowtiles, P.BH, P.qsplit), dim3(256), 0, st, a);
     const int64_t n = P.BH * (int64_t)P.geo.NS * D;
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D);
