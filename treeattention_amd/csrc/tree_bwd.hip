@@ -10,9 +10,8 @@
 // probabilities p_j receives, for every child j,
 //   G[n, j] = sum_{u under child j} dl_u  -  p_j * sum_{u under n} dl_u
 // (zero where the logit was clamped).  A query's distinct blocks are sorted,
-// so the blocks under any node are one contiguous run: the first block of the
-// run (the "leader") writes that node's b entries of G, summing in block
-// order -- no conflicts, no atomics.  Then
+// so the blocks under any node are one contiguous run, summed by segmented
+// scans with one writer per entry of G -- no conflicts, no atomics.  Then
 //   tree_dq_kernel: dq = sum_u dq_pair[u] + sum_chunks G C_chunk (MFMA); it
 //     also writes G^T and Q^T with the queries contiguous;
 //   tree_dc_kernel: dC = G^T Q per query split, a plain MFMA product of the
@@ -54,6 +53,7 @@ struct TreeArgs {
   void* dk;
   int64_t ksb, ksl, ksh;
   int qsplit;
+  int lp;  // log2 of S rounded up to a power of two
 };
 
 template <typename E>
@@ -96,9 +96,9 @@ __global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__
   if (act) dl[qh * S + u] = w * (dt - tot);
 }
 
-// Query tile of the dq kernel: the distinct leaf blocks of each query, their
-// dl and count (the Q rows live in registers as MFMA fragments).
-template <typename E, int D>
+// Query tile of the dq kernel in LDS: child logits of the current chunk, G of
+// the chunk, and each query's distinct leaf blocks, their dl and count.
+template <typename E>
 struct TileSmem {
   float* Xs;   // [64][kXS]
   E* Gm;       // [64][kGS]
@@ -107,14 +107,9 @@ struct TileSmem {
   int* cn;     // [64]
 };
 
-template <typename E, int D>
-__device__ __forceinline__ void load_tile(const TreeArgs& a, const TileSmem<E, D>& sm, RowFrags<E, D>& qf, int bb,
-                                          int h, int l0, int nq, int tid) {
-  const int lane = tid & 63, w = tid >> 6;
-  {
-    const int r = 16 * w + (lane & 15);
-    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
-  }
+template <typename E>
+__device__ __forceinline__ void load_slots(const TreeArgs& a, const TileSmem<E>& sm, int bb, int h, int l0, int nq,
+                                           int tid) {
   const int S = a.S;
   const int64_t qh0 = ((int64_t)bb * a.L + l0) * a.H + h;
   for (int e = tid; e < kQueryTile * S; e += 256) {
@@ -126,47 +121,128 @@ __device__ __forceinline__ void load_tile(const TreeArgs& a, const TileSmem<E, D
   if (tid < kQueryTile) sm.cn[tid] = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
 }
 
-// Leader-based G for depth d, chunk [c0, c0+ncols): G[qi*gq + col*gc].
+// G for depth d, chunk [c0, c0 + ncols) of the level's child rows, into
+// Gm[q][col].  A group of P = 2^lp >= S lanes per query, lane u = slot u
+// (slots ascend by leaf block, so the slots under one child row form a run,
+// and so do the slots under one node).  Segmented inclusive scans over the
+// runs give A_row (sum of dl under the child row) and A_n (under the node).
+// The last lane of each child run writes G[n, j] = A_row - p_j A_n; the last
+// lane of each node run writes -p_j A_n for the node's children without
+// sampled blocks.  Every entry has one writer and every sum a fixed order:
+// deterministic, no atomics.  Clamped logits get 0.
 template <typename E>
-__device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, int S, int nq, float maxhalf,
-                                        const float* Xs, const int* lf, const float* dls, const int* cn, E* Gm,
-                                        int gq, int gc, int tid) {
+__device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, int S, int lp, int nq,
+                                        float maxhalf, const float* Xs, const int* lf, const float* dls,
+                                        const int* cn, E* Gm, int tid) {
   const int b = G.b, lb = G.lb;
   const int sh = lb * (G.T - d), sh2 = sh - lb;
-  for (int e = tid; e < kQueryTile * S; e += 256) {
-    const int qi = e / S, u = e - qi * S;
-    if (qi >= nq || u >= cn[qi]) continue;
-    const int* L_ = lf + qi * S;
-    const int n = L_[u] >> sh;
-    if (u > 0 && (L_[u - 1] >> sh) == n) continue;
-    const int base = (n << lb) - c0;
-    if (base < 0 || base >= ncols) continue;
-    const float* D_ = dls + qi * S;
-    const int cnt = cn[qi];
-    int end = u + 1;
-    float V = D_[u];
-    while (end < cnt && (L_[end] >> sh) == n) V += D_[end++];
-    const float* xr = Xs + qi * kXS + base;
-    float mx = -__builtin_inff();
-    for (int j = 0; j < b; ++j) mx = fmaxf(mx, clamp_h(xr[j], maxhalf));
-    float se = 0.f;
-    for (int j = 0; j < b; ++j) se += __expf(clamp_h(xr[j], maxhalf) - mx);
-    const float lse = mx + __logf(se);
-    int v = u;
-    for (int j = 0; j < b; ++j) {
-      float Vj = 0.f;
-      while (v < end && ((L_[v] >> sh2) & (b - 1)) == j) Vj += D_[v++];
-      const float x = xr[j];
-      const bool live = x >= -maxhalf && x <= maxhalf;
-      const float p = __expf(clamp_h(x, maxhalf) - lse);
-      Gm[qi * gq + (base + j) * gc] = (E)(live ? Vj - p * V : 0.f);
+  const int P = 1 << lp;
+  const int lane = tid & 63;
+  for (int e0 = 0; e0 < (kQueryTile << lp); e0 += 256) {
+    const int e = e0 + tid;
+    const int qi = e >> lp, u = e & (P - 1);
+    const int cnt = qi < nq ? cn[qi] : 0;
+    const bool act = u < cnt;
+    const int leaf = act ? lf[qi * S + u] : 0;
+    const float dl = act ? dls[qi * S + u] : 0.f;
+    const int crow = act ? (leaf >> sh2) : -1 - u;  // inactive lanes: singleton runs
+    const int node = act ? (leaf >> sh) : -1 - u;
+    float vc = dl, vn = dl;
+    uint64_t has = act ? (1ull << (crow & (b - 1))) : 0ull;  // children of the node with sampled blocks
+    for (int o = 1; o < P; o <<= 1) {
+      const float tc = __shfl_up(vc, o, P);
+      const float tn = __shfl_up(vn, o, P);
+      const int kc = __shfl_up(crow, o, P);
+      const int kn = __shfl_up(node, o, P);
+      const uint64_t th = __shfl_up(has, o, P);
+      if (u >= o) {
+        if (kc == crow) vc += tc;
+        if (kn == node) {
+          vn += tn;
+          has |= th;
+        }
+      }
+    }
+    const int nxc = __shfl_down(crow, 1, P);
+    const int nxn = __shfl_down(node, 1, P);
+    const bool last = u + 1 >= cnt;
+    const bool cend = act && (last || nxc != crow);
+    const bool nend = act && (last || nxn != node);
+    const uint64_t rest = __ballot(nend) >> lane;
+    const int src = rest ? lane + __builtin_ctzll(rest) : lane;
+    const float An = __shfl(vn, src, 64);
+    const int base = (node << lb) - c0;
+    if ((cend || nend) && base >= 0 && base < ncols) {
+      const float* xr = Xs + qi * kXS + base;
+      float mx = -__builtin_inff();
+      for (int j = 0; j < b; ++j) mx = fmaxf(mx, clamp_h(xr[j], maxhalf));
+      float se = 0.f;
+      for (int j = 0; j < b; ++j) se += __expf(clamp_h(xr[j], maxhalf) - mx);
+      const float lse = mx + __logf(se);
+      E* gr = Gm + qi * kGS + base;
+      if (cend) {
+        const int j = crow & (b - 1);
+        const float x = xr[j];
+        const bool live = x >= -maxhalf && x <= maxhalf;
+        gr[j] = (E)(live ? vc - __expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
+      }
+      if (nend) {
+        for (int j = 0; j < b; ++j) {
+          if ((has >> j) & 1ull) continue;
+          const float x = xr[j];
+          const bool live = x >= -maxhalf && x <= maxhalf;
+          gr[j] = (E)(live ? -__expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
+        }
+      }
     }
   }
 }
 
+// acc[0..8) += sum_{u < n} rows[u*stride .. +8), in u order, with up to eight
+// rows' loads in flight.
+template <typename E>
+__device__ __forceinline__ void sum_rows8_deep(float* acc, const E* rows, int64_t stride, int n) {
+  for (int u0 = 0; u0 < n; u0 += 8) {
+    float x[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (u0 + j < n) {
+        const E* p = rows + (int64_t)(u0 + j) * stride;
+        if constexpr (sizeof(E) == 2) {
+          typedef __attribute__((ext_vector_type(8))) E v8;
+          const v8 v = *(const v8*)p;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[j][i] = (float)v[i];
+        } else {
+          const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+          x[j][0] = a.x; x[j][1] = a.y; x[j][2] = a.z; x[j][3] = a.w;
+          x[j][4] = b.x; x[j][5] = b.y; x[j][6] = b.z; x[j][7] = b.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[j][i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += x[j][i];
+  }
+}
+
+// One workgroup per 64 queries of one (batch, head).  All 64 query rows are
+// held by every wave as MFMA fragments.  Per chunk of a level's child rows:
+//   X^T = C_chunk Q^T   (wave w: column tiles w, w+4, ...; C rows from global)
+//   G   = build_g(X)    (LDS)
+//   dq^T += C_chunk^T G^T (wave w: head-dim tiles w, w+4, ...)
+// and G^T goes to global for the summary-gradient product.  The epilogue adds
+// the leaf parts dq_pair of each query's distinct blocks.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
   using M = Mfma<E>;
+  using F = typename M::frag;
+  constexpr int KS = D / M::K;
+  constexpr int NMD = (D / 16 + 3) / 4;  // head-dim tiles per wave
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
@@ -176,48 +252,69 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
   const int64_t rows = G.NS;
 
-  TileSmem<E, D> sm;
+  TileSmem<E> sm;
   sm.Xs = (float*)smem;
   sm.Gm = (E*)(sm.Xs + kQueryTile * kXS);
   sm.lf = (int*)(sm.Gm + kQueryTile * kGS);
   sm.dls = (float*)(sm.lf + kQueryTile * S);
   sm.cn = (int*)(sm.dls + kQueryTile * S);
 
-  RowFrags<E, D> qf;
-  load_tile<E, D>(a, sm, qf, bb, h, l0, nq, tid);
-  {
-    // Q^T for the summary-gradient product (rows past nq are zero fragments)
-    E* qt = (E*)a.qt + (int64_t)bh * D * a.Lp + l0 + 16 * w + col;
+  RowFrags<E, D> qa[4];
 #pragma unroll
-    for (int ks = 0; ks < D / M::K; ++ks) {
+  for (int qt = 0; qt < 4; ++qt) {
+    const int r = 16 * qt + col;
+    qa[qt].load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, g);
+  }
+  load_slots<E>(a, sm, bb, h, l0, nq, tid);
+  // Q^T for the summary-gradient product (rows past nq are zero fragments)
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    if (qt != w) continue;
+    E* qt_out = (E*)a.qt + (int64_t)bh * D * a.Lp + l0 + 16 * qt + col;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
       if constexpr (M::KPL == 1) {
-        qt[(int64_t)(ks * M::K + g) * a.Lp] = qf.f[ks];
+        qt_out[(int64_t)(ks * M::K + g) * a.Lp] = qa[qt].f[ks];
       } else {
 #pragma unroll
-        for (int i = 0; i < M::KPL; ++i) qt[(int64_t)(ks * M::K + M::KPL * g + i) * a.Lp] = qf.f[ks][i];
+        for (int i = 0; i < M::KPL; ++i) qt_out[(int64_t)(ks * M::K + M::KPL * g + i) * a.Lp] = qa[qt].f[ks][i];
       }
     }
   }
-  __syncthreads();
 
-  f32x4 dacc[D / 16];
+  f32x4 dacc[NMD][4];
 #pragma unroll
-  for (int nd = 0; nd < D / 16; ++nd) dacc[nd] = zero4();
+  for (int i = 0; i < NMD; ++i)
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) dacc[i][qt] = zero4();
   const E* sum_hi = (const E*)a.sum_hi;
   const E* sum_t = (const E*)a.sum_t;
   for (int d = 0; d < T; ++d) {
     const int lam = d + 1, lvl = G.pw[lam];
     for (int c0 = 0; c0 < lvl; c0 += kChunk) {
       const int ncols = min(kChunk, lvl - c0);
-      const int kcols = (ncols + 31) / 32 * 32;
+      const int kcols = (ncols + 31) / 32 * 32;  // inside the level's zero padding
       const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
-      mfma_rows<E, D, false>(qf, sm.Xs, kXS, sum_hi, nullptr, r0, ncols, r0, lane, w);
+      // X^T tiles: rows of C (this wave's column tiles) against all 64 queries
+      for (int ct = w; ct < kcols / 16; ct += 4) {
+        const E* ar = sum_hi + (r0 + 16 * ct + col) * D + M::KPL * g;
+        F af[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) af[ks] = ld_frag(ar + ks * M::K);
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          f32x4 c = zero4();
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) c = M::mma(af[ks], qa[qt].f[ks], c);
+          *(f32x4*)(sm.Xs + (16 * qt + col) * kXS + 16 * ct + 4 * g) = c;
+        }
+      }
       for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
         const int r = e / (kcols / 8), c = (e - r * (kcols / 8)) * 8;
         z8(sm.Gm + r * kGS + c);
       }
       __syncthreads();
-      build_g<E>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, kGS, 1, tid);
+      build_g<E>(G, d, c0, ncols, S, a.lp, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
       __syncthreads();
       {
         // G^T rows of the chunk (kcols covers the level's zero padding rows),
@@ -231,25 +328,36 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
           cp8(gt + (int64_t)c * a.Lp + q0, v8);
         }
       }
-      const int ksteps = kcols / M::K;
-      const E* ap = sm.Gm + (16 * w + col) * kGS + M::KPL * g;
-      const E* bp = sum_t + ((int64_t)bh * D + col) * rows + G.off[lam] + c0 + M::KPL * g;
-      for (int ks = 0; ks < ksteps; ++ks) {
-        const auto af = ld_frag(ap + ks * M::K);
+      // dq^T += C^T G^T: A = C^T rows (head dims, from global), B = G rows (LDS)
+      for (int ks = 0; ks < kcols / M::K; ++ks) {
+        F bg[4];
 #pragma unroll
-        for (int nd = 0; nd < D / 16; ++nd)
-          dacc[nd] = M::mma(af, ld_frag(bp + (int64_t)16 * nd * rows + ks * M::K), dacc[nd]);
+        for (int qt = 0; qt < 4; ++qt) bg[qt] = ld_frag(sm.Gm + (16 * qt + col) * kGS + ks * M::K + M::KPL * g);
+#pragma unroll
+        for (int i = 0; i < NMD; ++i) {
+          const int md = w + 4 * i;
+          if (md < D / 16) {
+            const F at = ld_frag(sum_t + ((int64_t)bh * D + 16 * md + col) * rows + G.off[lam] + c0 + ks * M::K +
+                                 M::KPL * g);
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt) dacc[i][qt] = M::mma(at, bg[qt], dacc[i][qt]);
+          }
+        }
       }
       __syncthreads();
     }
   }
-  // stage the tree dq, add the leaf parts, write
+  // stage the tree dq as [q][d], add the leaf parts, write
   constexpr int SS = D + 4;
   float* stage = sm.Xs;  // [64][D+4] fits in [64][kXS]
 #pragma unroll
-  for (int nd = 0; nd < D / 16; ++nd)
+  for (int i = 0; i < NMD; ++i) {
+    const int md = w + 4 * i;
+    if (md < D / 16) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) stage[(16 * w + 4 * g + r) * SS + 16 * nd + col] = dacc[nd][r];
+      for (int qt = 0; qt < 4; ++qt) *(f32x4*)(stage + (16 * qt + col) * SS + 16 * md + 4 * g) = dacc[i][qt];
+    }
+  }
   __syncthreads();
   const E* dqp = (const E*)a.dq_part;
   E* dq = (E*)a.dq;
@@ -260,7 +368,7 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = stage[qi * SS + d0 + i];
-    sum_rows8(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
+    sum_rows8_deep(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
     E* o = dq + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + d0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = (E)acc[i];
@@ -430,6 +538,8 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.dk = dk;
   a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
   a.qsplit = P.qsplit;
+  a.lp = 0;
+  while ((1 << a.lp) < P.S) ++a.lp;
 
   const int64_t nqh = P.B * P.L * P.H;
   int pw2 = 1;
