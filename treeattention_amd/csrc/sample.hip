@@ -3,16 +3,23 @@
 // Generalizes _sample_paths_non_causal (_tree_mha.py:78-122) and the
 // treeattn-cuda step kernel (sample_non_causal_paths.cu:54-128) to b-ary trees
 // with leaf blocks.  One workgroup owns 64 consecutive queries of one
-// (batch, head).  Per depth, the child logits of every node of that level are
-// an MFMA tile Q (64 x D) x summaries^T staged in LDS (summaries split into
-// hi + lo parts of the input type so the logits are float-accurate); then each
-// (query, sample) takes its decision from LDS:
-//   logp_j = log_softmax(clamp(x_j, +-max_logit/2)),  plus the causal
-//   correction on the boundary path, direction = argmax_j(logp_j + g_j)
-//   (first maximum wins), g = -log(-log u) from the caller's uniforms or the
-// counter RNG.  Finally one wavefront per query (lane = sample) writes the
-// softmax weights over samples (_tree_mha.py:396-399) and the ascending list
-// of distinct sampled leaf blocks with their summed weights.
+// (batch, head); every thread owns a fixed set of (query, sample) items whose
+// current node and accumulated log-probability stay in registers for the
+// whole walk.  Per depth:
+//   1. the child logits of every node of the level that the tile can reach
+//      are one MFMA product  C_level (rows) x Q^T (64 queries), each wave
+//      taking every fourth 16-row tile of C for all 64 queries, so every
+//      summary row is read once per workgroup.  Summaries are split into
+//      hi + lo parts of the input type so the logits are float-accurate.
+//      The tile lands in LDS as X[query][child].
+//   2. each item reads its node's b child logits from LDS and decides:
+//        logp_j = log_softmax(clamp(x_j, +-max_logit/2))  (+ the causal
+//        correction on the boundary path),
+//        direction = argmax_j(logp_j + g_j), first maximum wins,
+//      with g = -log(-log u) from the caller's uniforms or the counter RNG.
+// Finally each item computes its sample weight (softmax over the query's
+// samples, _tree_mha.py:396-399) and the query's ascending distinct leaf
+// blocks with their summed weights, through LDS.
 #include "launch.h"
 
 namespace ta {
@@ -36,210 +43,431 @@ struct SampleArgs {
   int* slot_count;
 };
 
-constexpr int kDoneBit = 1 << 30;
-constexpr int kXS = kChunk + 4;  // padded row stride (floats) of the logit tile
+constexpr int kLevelCols = 256;          // child columns of one level pass
+constexpr int kXS = kLevelCols + 4;      // padded row stride (floats) of the logit tile
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float clampf(float x, float m) { return fminf(fmaxf(x, -m), m); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <typename E, int D>
+// Child-logit products of one pass: up to kLevelCols/16 column tiles, tile t
+// being the 16 summary rows from row(t) (rows past a level's nodes are zero
+// padding); X[q][16t + c] = q . C[row(t) + c] for all 64 queries of the
+// workgroup.  Wave w computes tiles w, w+4, ...; the next tile's summary
+// fragments are loaded while the current tile's MFMAs run, and the first
+// tile of the next pass is loaded (prefetch) before the caller consumes the
+// current one.
+template <typename E, int D, bool kLo>
+struct LogitPipe {
+  using M = Mfma<E>;
+  using F = typename M::frag;
+  static constexpr int KS = D / M::K;
+  F ah[KS], al[KS];
+  int64_t rmax;  // last valid summary row: tile rows past it read it (results unused)
+
+  __device__ __forceinline__ void load(const E* hi, const E* lo, int64_t row, int lane, F (&h)[KS], F (&l)[KS]) {
+    const int64_t r = min(row + (lane & 15), rmax);
+    const int64_t rb = r * D + M::KPL * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      h[ks] = ld_frag(hi + rb + ks * M::K);
+      if constexpr (kLo) l[ks] = ld_frag(lo + rb + ks * M::K);
+    }
+  }
+
+  template <class RowFn>
+  __device__ __forceinline__ void prefetch(const E* hi, const E* lo, RowFn row, int ntiles, int lane, int w) {
+    if (w < ntiles) load(hi, lo, row(w), lane, ah, al);
+  }
+
+  template <class RowFn>
+  __device__ __forceinline__ void run(const RowFrags<E, D> (&qa)[4], float* Xs, const E* hi, const E* lo, RowFn row,
+                                      int ntiles, int lane, int w) {
+    const int col = lane & 15, g = lane >> 4;
+    for (int ct = w; ct < ntiles; ct += 4) {
+      F nh[KS], nl[KS];
+      if (ct + 4 < ntiles) load(hi, lo, row(ct + 4), lane, nh, nl);
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        f32x4 c = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          c = M::mma(ah[ks], qa[qt].f[ks], c);
+          if constexpr (kLo) c = M::mma(al[ks], qa[qt].f[ks], c);
+        }
+        *(f32x4*)(Xs + (16 * qt + col) * kXS + 16 * ct + 4 * g) = c;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        ah[ks] = nh[ks];
+        if constexpr (kLo) al[ks] = nl[ks];
+      }
+    }
+  }
+};
+
+// The passes of one workgroup, in order: causal boundary batches (the
+// boundary-path children of every depth, 16 column tiles per batch), then
+// every level in chunks of kLevelCols children (causal: only children of
+// nodes that contain a reachable leaf block).
+struct Passes {
+  int T, lb, causal, blk_lo, blk_hi, nbt;  // nbt: causal boundary tiles
+  const Geo* G;
+  int64_t base;                             // first summary row of this (batch, head)
+
+  // depth d's boundary children: columns [c0, c0 + ncols) of level d + 1
+  __device__ __forceinline__ int bc0(int d) const { return (blk_lo >> (lb * (T - d))) << lb; }
+  __device__ __forceinline__ int bcols(int d) const {
+    const int sh = lb * (T - d);
+    return ((blk_hi >> sh) - (blk_lo >> sh) + 1) << lb;
+  }
+  __device__ __forceinline__ int btiles(int d) const { return (bcols(d) + 15) >> 4; }
+  __device__ __forceinline__ int level_cols(int d) const {
+    int n = G->pw[d + 1];
+    if (causal) n = min(n, ((blk_hi >> (lb * (T - d))) + 1) << lb);
+    return n;
+  }
+  __device__ __forceinline__ int nbatch() const { return (nbt + kLevelCols / 16 - 1) / (kLevelCols / 16); }
+  // summary row of global boundary tile t
+  __device__ __forceinline__ int64_t brow(int t) const {
+    int d = 0, t0 = 0;
+    while (t >= t0 + btiles(d)) {
+      t0 += btiles(d);
+      ++d;
+    }
+    return base + G->off[d + 1] + bc0(d) + 16 * (t - t0);
+  }
+};
+
+// Uniform `idx` of the (B, L, H, S, T, b) tensor: from the caller's tensor,
+// else word idx%4 of Philox(idx/4).  The last Philox block is cached per item.
+struct RngCache {
+  uint64_t ctr;
+  uint32_t w0, w1, w2, w3;
+};
+
+__device__ __forceinline__ float uniform_at(const float* U, uint64_t seed, int64_t idx, RngCache& rc) {
+  if (U) return U[idx];
+  const uint64_t ctr = (uint64_t)idx >> 2;
+  if (ctr != rc.ctr) {
+    const Philox4 ph = philox4x32_10(ctr, seed);
+    rc.ctr = ctr;
+    rc.w0 = ph.w[0]; rc.w1 = ph.w[1]; rc.w2 = ph.w[2]; rc.w3 = ph.w[3];
+  }
+  const int wi = (int)(idx & 3);
+  return word_to_uniform(wi == 0 ? rc.w0 : wi == 1 ? rc.w1 : wi == 2 ? rc.w2 : rc.w3);
+}
+
+// kB: branching known at compile time (2 or 4), or 0 for the runtime value.
+// kNI: (query, sample) items per thread, >= 64 * S / 256.
+template <typename E, int D, int kB, int kNI>
 __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
   const int l0 = blockIdx.x * kQueryTile;
   const int nq = min(kQueryTile, a.L - l0);
-  const int S = a.S, T = G.T, b = G.b, lb = G.lb;
+  const int S = a.S, T = G.T, lb = G.lb;
+  const int b = kB ? kB : G.b;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t rows = G.NS;
   constexpr bool kLo = sizeof(E) == 2;
 
-  float* Xs = (float*)smem;
-  int* node = (int*)(Xs + kQueryTile * kXS);
-  float* acc = (float*)(node + kQueryTile * S);
-  float* logA = acc + kQueryTile * S;        // [64][T+1]
-  float* xb = logA + kQueryTile * (T + 1);   // [64][T*b]
+  float* Xs = (float*)smem;                      // [64][kXS] logits of one level pass
+  float* logA = Xs + kQueryTile * kXS;           // [64][T+1] causal boundary log-mass
+  float* xb = logA + kQueryTile * (T + 1);       // [64][T*b] boundary child logits
+  // after the walk Xs is reused: leaf, log-prob and distinct-leaf key per item
+  int* lf = (int*)Xs;
+  float* lps = Xs + kQueryTile * S;
+  int* fl = (int*)(Xs + 2 * kQueryTile * S);
 
-  // this wave's 16 query rows stay in registers as MFMA A fragments
-  RowFrags<E, D> qf;
-  {
-    const int r = 16 * w + (lane & 15);
-    qf.load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
+  // all 64 query rows as MFMA B fragments (rows past nq are zero)
+  RowFrags<E, D> qa[4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int r = 16 * qt + (lane & 15);
+    qa[qt].load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
   }
-  for (int e = tid; e < kQueryTile * S; e += 256) {
-    node[e] = 0;
-    acc[e] = 0.f;
-  }
-  __syncthreads();
-
   const E* hi = (const E*)(sizeof(E) == 2 ? a.sum_hi : (const void*)a.sum32);
   const E* lo = (const E*)a.sum_lo;
 
-  // Causal: allowed log-mass of each boundary-path node, bottom-up:
-  // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.  The boundary nodes of
-  // consecutive queries form one contiguous node range per depth, so their
-  // child logits come from the same MFMA tile as the walk's.
-  if (a.causal && T > 0) {
-    const int nb = T * b;
-    const int blk_lo = (l0 + a.coff) / G.LB, blk_hi = (l0 + nq - 1 + a.coff) / G.LB;
-    for (int d = 0; d < T; ++d) {
-      const int sh = lb * (T - d);
-      const int c0 = (blk_lo >> sh) << lb;
-      const int ncols = (((blk_hi >> sh) + 1) << lb) - c0;
-      for (int cc = 0; cc < ncols; cc += kChunk) {
-        const int nc = min(kChunk, ncols - cc);
-        const int64_t r0 = (int64_t)bh * rows + G.off[d + 1] + c0 + cc;
-        mfma_rows<E, D, kLo>(qf, Xs, kXS, hi, lo, r0, nc, r0, lane, w);
-        __syncthreads();
-        for (int qi = tid; qi < nq; qi += 256) {
-          const int blk = (l0 + qi + a.coff) / G.LB;
-          const int col = ((blk >> sh) << lb) - c0 - cc;
-          if (col >= 0 && col < nc)
-            for (int j = 0; j < b; ++j) xb[qi * nb + d * b + j] = clampf(Xs[qi * kXS + col + j], a.maxhalf);
-        }
-        __syncthreads();
-      }
-    }
-    if (tid < nq) {
-      const int blk = (l0 + tid + a.coff) / G.LB;
-      float* la = logA + tid * (T + 1);
-      la[T] = 0.f;
-      for (int d = T - 1; d >= 0; --d) {
-        const int js = (blk >> (lb * (T - 1 - d))) & (b - 1);
-        const float* xs = xb + tid * nb + d * b;
-        float mx = -__builtin_inff();
-        for (int j = 0; j < b; ++j) mx = fmaxf(mx, xs[j]);
-        float se = 0.f;
-        for (int j = 0; j < b; ++j) se += expf(xs[j] - mx);
-        const float lse = mx + logf(se);
-        // terms: logp_j (j < js), logp_js + logA_{d+1}
-        float tm = -__builtin_inff();
-        for (int j = 0; j <= js; ++j) tm = fmaxf(tm, xs[j] - lse + (j == js ? la[d + 1] : 0.f));
-        float ts = 0.f;
-        for (int j = 0; j <= js; ++j) ts += expf(xs[j] - lse + (j == js ? la[d + 1] : 0.f) - tm);
-        la[d] = tm + logf(ts);
-      }
-    }
-    __syncthreads();
+  Passes ps;
+  ps.T = T;
+  ps.lb = lb;
+  ps.causal = a.causal && T > 0;
+  // leaf blocks [0, blk_hi] are reachable from some query of the tile
+  ps.blk_lo = (l0 + a.coff) / G.LB;
+  ps.blk_hi = (l0 + nq - 1 + a.coff) / G.LB;
+  ps.G = &G;
+  ps.base = (int64_t)bh * rows;
+  ps.nbt = 0;
+  if (ps.causal)
+    for (int d = 0; d < T; ++d) ps.nbt += ps.btiles(d);
+  const int nbatch = ps.causal ? ps.nbatch() : 0;
+
+  // items: i = tid + 256 k -> (query i / S, sample i % S); node, log-prob,
+  // the causal boundary leaf block, the uniforms' base index and (binary
+  // trees) the last Philox block stay in registers
+  const int nitems = kQueryTile * S;
+  int node[kNI], iq[kNI], is[kNI], iblk[kNI];
+  int64_t ubase[kNI];
+  float acc[kNI];
+  constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
+  RngCache rc[kNC];
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    node[k] = 0;
+    acc[k] = 0.f;
+    iq[k] = it < nitems ? it / S : kQueryTile;
+    is[k] = it < nitems ? it - iq[k] * S : 0;
+    if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
+    const int l = l0 + min(iq[k], nq - 1);
+    iblk[k] = (l + a.coff) / G.LB;
+    ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
+  }
+#pragma unroll
+  for (int k = 0; k < kNC; ++k) {
+    rc[k].ctr = ~0ull;
+    rc[k].w0 = rc[k].w1 = rc[k].w2 = rc[k].w3 = 0u;
   }
 
-  for (int d = 0; d < T; ++d) {
-    const int lam = d + 1, lvl = G.pw[lam];
-    for (int c0 = 0; c0 < lvl; c0 += kChunk) {
-      const int ncols = min(kChunk, lvl - c0);
-      const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
-      mfma_rows<E, D, kLo>(qf, Xs, kXS, hi, lo, r0, ncols, r0, lane, w);
-      __syncthreads();
-      for (int it = tid; it < kQueryTile * S; it += 256) {
-        const int qi = it / S;
-        if (qi >= nq) continue;
-        const int i = node[it];
-        if (i & kDoneBit) continue;
-        const int base = (i << lb) - c0;
+  // pass p < nbatch: causal boundary batch p; then level d, chunk c0
+  LogitPipe<E, D, kLo> pipe;
+  pipe.rmax = ps.base + rows - 1;
+  auto tiles_of = [&](int p, int d, int c0) {
+    if (p < nbatch) return min(kLevelCols / 16, ps.nbt - p * (kLevelCols / 16));
+    return (min(kLevelCols, ps.level_cols(d) - c0) + 15) >> 4;
+  };
+  auto prefetch = [&](int p, int d, int c0) {
+    if (p < nbatch) {
+      const int t0 = p * (kLevelCols / 16);
+      pipe.prefetch(hi, lo, [&](int t) { return ps.brow(t0 + t); }, tiles_of(p, d, c0), lane, w);
+    } else {
+      const int64_t r0 = ps.base + G.off[d + 1] + c0;
+      pipe.prefetch(hi, lo, [&](int t) { return r0 + 16 * t; }, tiles_of(p, d, c0), lane, w);
+    }
+  };
+  int p = 0, d = 0, c0 = 0;  // current pass
+  if (T > 0) prefetch(0, 0, 0);
+  while (p < nbatch || d < T) {
+    const int nt = tiles_of(p, d, c0);
+    if (p < nbatch) {
+      const int t0 = p * (kLevelCols / 16);
+      pipe.run(qa, Xs, hi, lo, [&](int t) { return ps.brow(t0 + t); }, nt, lane, w);
+    } else {
+      const int64_t r0 = ps.base + G.off[d + 1] + c0;
+      pipe.run(qa, Xs, hi, lo, [&](int t) { return r0 + 16 * t; }, nt, lane, w);
+    }
+    __syncthreads();
+    // next pass, and its first tile in flight while this one is consumed
+    int np = p + 1, nd = d, nc0 = c0;
+    if (p >= nbatch) {
+      nc0 = c0 + kLevelCols;
+      if (nc0 >= ps.level_cols(d)) {
+        nc0 = 0;
+        ++nd;
+      }
+    }
+    if (np < nbatch || nd < T) prefetch(np, nd, nc0);
+
+    if (p < nbatch) {
+      // boundary child logits of this batch's depths
+      if (tid < nq) {
+        const int blk = (l0 + tid + a.coff) / G.LB;
+        int t0 = 0;
+        for (int dd = 0; dd < T; ++dd) {
+          // column of the query's boundary node's first child in the global tile space
+          const int gc = 16 * t0 + ((blk >> (lb * (T - dd))) << lb) - ps.bc0(dd) - p * kLevelCols;
+          if (gc >= 0 && gc < kLevelCols)
+            for (int j = 0; j < b; ++j) xb[tid * T * b + dd * b + j] = clampf(Xs[tid * kXS + gc + j], a.maxhalf);
+          t0 += ps.btiles(dd);
+        }
+      }
+      if (p + 1 == nbatch) {
+        // Causal: allowed log-mass of each boundary-path node, bottom-up:
+        // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.
+        __syncthreads();
+        if (tid < nq) {
+          const int blk = (l0 + tid + a.coff) / G.LB;
+          float* la = logA + tid * (T + 1);
+          la[T] = 0.f;
+          for (int dd = T - 1; dd >= 0; --dd) {
+            const int js = (blk >> (lb * (T - 1 - dd))) & (b - 1);
+            const float* xs = xb + tid * T * b + dd * b;
+            float mx = -__builtin_inff();
+            for (int j = 0; j < b; ++j) mx = fmaxf(mx, xs[j]);
+            float se = 0.f;
+            for (int j = 0; j < b; ++j) se += expf(xs[j] - mx);
+            const float lse = mx + logf(se);
+            // terms: logp_j (j < js), logp_js + logA_{d+1}
+            float tm = -__builtin_inff();
+            for (int j = 0; j <= js; ++j) tm = fmaxf(tm, xs[j] - lse + (j == js ? la[dd + 1] : 0.f));
+            float ts = 0.f;
+            for (int j = 0; j <= js; ++j) ts += expf(xs[j] - lse + (j == js ? la[dd + 1] : 0.f) - tm);
+            la[dd] = tm + logf(ts);
+          }
+        }
+      }
+    } else {
+      const int ncols = min(kLevelCols, ps.level_cols(d) - c0);
+      const int shb = lb * (T - d), shc = lb * (T - 1 - d);
+#pragma unroll
+      for (int k = 0; k < kNI; ++k) {
+        const int qi = iq[k];
+        if (qi >= kQueryTile) continue;
+        const int base = (node[k] << lb) - c0;
         if (base < 0 || base >= ncols) continue;
-        const int s = it - qi * S;
         const float* xr = Xs + qi * kXS + base;
-        float mx = -__builtin_inff();
-        for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
-        float se = 0.f;
-        for (int j = 0; j < b; ++j) se += expf(clampf(xr[j], a.maxhalf) - mx);
-        const float lse = mx + logf(se);
+        // log-sum-exp of the clamped child logits
+        float lse;
+        float x[kB ? kB : 1];
+        if constexpr (kB != 0) {
+          float mx = -__builtin_inff();
+#pragma unroll
+          for (int j = 0; j < kB; ++j) {
+            x[j] = clampf(xr[j], a.maxhalf);
+            mx = fmaxf(mx, x[j]);
+          }
+          float se = 0.f;
+#pragma unroll
+          for (int j = 0; j < kB; ++j) se += fast_exp2((x[j] - mx) * kLog2e);
+          lse = mx + fast_log2(se) * kLn2;
+        } else {
+          float mx = -__builtin_inff();
+          for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
+          float se = 0.f;
+          for (int j = 0; j < b; ++j) se += fast_exp2((clampf(xr[j], a.maxhalf) - mx) * kLog2e);
+          lse = mx + fast_log2(se) * kLn2;
+        }
         bool onb = false;
         int js = 0;
         float la_d = 0.f, la_c = 0.f;
-        if (a.causal) {
-          const int blk = (l0 + qi + a.coff) / G.LB;
-          if ((blk >> (lb * (T - d))) == i) {
-            onb = true;
-            js = (blk >> (lb * (T - 1 - d))) & (b - 1);
-            la_d = logA[qi * (T + 1) + d];
-            la_c = logA[qi * (T + 1) + d + 1];
-          }
+        if (a.causal && (iblk[k] >> shb) == node[k]) {
+          onb = true;
+          js = (iblk[k] >> shc) & (b - 1);
+          la_d = logA[qi * (T + 1) + d];
+          la_c = logA[qi * (T + 1) + d + 1];
         }
-        const int64_t ubase = (((((int64_t)bb * a.L + l0 + qi) * a.H + h) * S + s) * T + d) * b;
-        uint64_t cached = ~0ull;
-        Philox4 ph;
+        const int64_t ub = ubase[k] + d * b;
+        RngCache local;
+        local.ctr = ~0ull;
+        local.w0 = local.w1 = local.w2 = local.w3 = 0u;
+        RngCache& cache = kB == 2 ? rc[kB == 2 ? k : 0] : local;
         float best = -__builtin_inff(), bl = 0.f;
         int bj = 0;
-        for (int j = 0; j < b; ++j) {
-          float lp = clampf(xr[j], a.maxhalf) - lse;
+        auto consider = [&](int j, float xj) {
+          float lp = xj - lse;
           if (onb) {
             if (j < js) lp -= la_d;
             else if (j == js) lp += la_c - la_d;
             else lp = -__builtin_inff();
           }
-          float u;
-          if (a.U) {
-            u = a.U[ubase + j];
-          } else {
-            const int64_t idx = ubase + j;
-            const uint64_t ctr = (uint64_t)idx >> 2;
-            if (ctr != cached) {
-              ph = philox4x32_10(ctr, a.seed);
-              cached = ctr;
-            }
-            const int wi = (int)(idx & 3);
-            u = word_to_uniform(wi == 0 ? ph.w[0] : wi == 1 ? ph.w[1] : wi == 2 ? ph.w[2] : ph.w[3]);
-          }
-          const float sc = lp - logf(-logf(u));
+          const float u = uniform_at(a.U, a.seed, ub + j, cache);
+          // lp + g up to the common constant -log(ln 2): g = -ln(ln2 * -log2 u)
+          const float sc = lp - kLn2 * fast_log2(-fast_log2(u));
           if (sc > best) {
             best = sc;
             bj = j;
             bl = lp;
           }
+        };
+        if constexpr (kB != 0) {
+#pragma unroll
+          for (int j = 0; j < kB; ++j) consider(j, x[j]);
+        } else {
+          for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
         }
-        node[it] = ((i << lb) + bj) | kDoneBit;
-        acc[it] += bl;
+        node[k] = (node[k] << lb) + bj;
+        acc[k] += bl;
       }
-      __syncthreads();
     }
-    for (int it = tid; it < kQueryTile * S; it += 256) node[it] &= ~kDoneBit;
     __syncthreads();
+    p = np;
+    d = nd;
+    c0 = nc0;
   }
 
-  // weights and distinct leaf blocks, one wavefront per query
-  for (int qi = w; qi < nq; qi += 4) {
+  // weights (softmax over the query's samples) and distinct leaf blocks
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    if (it < nitems) {
+      lf[it] = node[k];
+      lps[it] = acc[k];
+    }
+  }
+  __syncthreads();
+  float wgt[kNI];
+  bool first[kNI];
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    wgt[k] = 0.f;
+    first[k] = false;
+    const int qi = iq[k];
+    if (qi >= kQueryTile) continue;
+    const int s = is[k];
+    const int* lq = lf + qi * S;
+    const float* pq = lps + qi * S;
+    float m = -__builtin_inff();
+    for (int j = 0; j < S; ++j) m = fmaxf(m, pq[j]);
+    float sum = 0.f, tot = 0.f;
+    bool fst = true;
+    for (int j = 0; j < S; ++j) {
+      const float e = fast_exp2((pq[j] - m) * kLog2e);
+      sum += e;
+      if (lq[j] == node[k]) {
+        if (j < s) fst = false;
+        else tot += e;
+      }
+    }
+    const float inv = 1.f / sum;
+    wgt[k] = fast_exp2((acc[k] - m) * kLog2e) * inv;
+    first[k] = fst;
+    acc[k] = tot * inv;  // summed weight of this leaf block (used if first)
+  }
+  // distinct-leaf keys: the leaf for a first occurrence, else INT_MAX
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    if (iq[k] < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
+    else if (it < nitems) fl[it] = 0x7fffffff;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int qi = iq[k];
+    if (qi >= kQueryTile) continue;
+    const int s = is[k];
     const int l = l0 + qi;
     const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    const bool act = lane < S;
-    const int beta = act ? node[qi * S + lane] : 0x7fffffff;
-    const float lp = act ? acc[qi * S + lane] : -__builtin_inff();
-    const float m = wave_max(lp);
-    const float ex = act ? expf(lp - m) : 0.f;
-    const float wgt = ex / wave_sum(ex);
-    if (act) {
-      a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + lane] = wgt;
-      a.leaf[qh * S + lane] = beta;
+    a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = wgt[k];
+    a.leaf[qh * S + s] = node[k];
+    const int* fq = fl + qi * S;
+    if (first[k]) {
+      int rank = 0;
+      for (int j = 0; j < S; ++j) rank += fq[j] < node[k];
+      a.slot_leaf[qh * S + rank] = node[k];
+      a.slot_weight[qh * S + rank] = acc[k];
     }
-    bool first = act;
-    for (int j = 0; j < S; ++j) {
-      const int bj = __shfl(beta, j, 64);
-      if (j < lane && bj == beta) first = false;
+    if (s == 0) {
+      int cnt = 0;
+      for (int j = 0; j < S; ++j) cnt += fq[j] != 0x7fffffff;
+      a.slot_count[qh] = cnt;
     }
-    int rank = 0, cnt = 0;
-    float tot = 0.f;
-    for (int j = 0; j < S; ++j) {
-      const int bj = __shfl(beta, j, 64);
-      const int fj = __shfl((int)first, j, 64);
-      const float wj = __shfl(wgt, j, 64);
-      if (fj && bj < beta) ++rank;
-      cnt += fj;
-      if (bj == beta && j >= lane) tot += wj;
-    }
-    if (first) {
-      a.slot_leaf[qh * S + rank] = beta;
-      a.slot_weight[qh * S + rank] = tot;
-    }
-    if (lane == 0) a.slot_count[qh] = cnt;
   }
 }
 
+// Xs (which the final phase's three [64][S] arrays alias: 3 * 64 * 64 * 4
+// bytes < sizeof Xs), logA and the boundary child logits.
 int sample_smem(const Plan& P) {
   const int T = P.geo.T, b = P.geo.b;
-  return kQueryTile * kXS * 4 + kQueryTile * (int)P.S * 8 +
-         kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
+  return kQueryTile * kXS * 4 + kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
 }
 
-template <typename E, int D>
+template <typename E, int D, int kB, int kNI>
 static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
                               char* rec, hipStream_t st) {
   SampleArgs a;
@@ -268,22 +496,37 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.slot_weight = (float*)(rec + P.rec.slot_weight);
   a.slot_count = (int*)(rec + P.rec.slot_count);
   const int smem = sample_smem(P);
-  hipError_t e = hipFuncSetAttribute((const void*)sample_kernel<E, D>,
+  hipError_t e = hipFuncSetAttribute((const void*)sample_kernel<E, D, kB, kNI>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sample_kernel<E, D>), dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH),
+  hipLaunchKernelGGL((sample_kernel<E, D, kB, kNI>), dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH),
                      dim3(256), smem, st, a);
   return hipGetLastError();
+}
+
+template <typename E, int D>
+static hipError_t sample_b(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
+                           hipStream_t st) {
+  static_assert(kMaxSamples * kQueryTile / 256 == 16, "items per thread");
+  const bool few = P.S <= 16;  // 64 * S / 256 <= 4 items per thread
+  switch (P.geo.b) {
+    case 2: return few ? sample_impl<E, D, 2, 4>(P, q, U, seed, w, rec, st)
+                       : sample_impl<E, D, 2, 16>(P, q, U, seed, w, rec, st);
+    case 4: return few ? sample_impl<E, D, 4, 4>(P, q, U, seed, w, rec, st)
+                       : sample_impl<E, D, 4, 16>(P, q, U, seed, w, rec, st);
+    default: return few ? sample_impl<E, D, 0, 4>(P, q, U, seed, w, rec, st)
+                        : sample_impl<E, D, 0, 16>(P, q, U, seed, w, rec, st);
+  }
 }
 
 template <typename E>
 static hipError_t sample_d(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
                            hipStream_t st) {
   switch (P.D) {
-    case 32: return sample_impl<E, 32>(P, q, U, seed, w, rec, st);
-    case 64: return sample_impl<E, 64>(P, q, U, seed, w, rec, st);
-    case 96: return sample_impl<E, 96>(P, q, U, seed, w, rec, st);
-    default: return sample_impl<E, 128>(P, q, U, seed, w, rec, st);
+    case 32: return sample_b<E, 32>(P, q, U, seed, w, rec, st);
+    case 64: return sample_b<E, 64>(P, q, U, seed, w, rec, st);
+    case 96: return sample_b<E, 96>(P, q, U, seed, w, rec, st);
+    default: return sample_b<E, 128>(P, q, U, seed, w, rec, st);
   }
 }
 
