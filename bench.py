@@ -73,12 +73,13 @@ def tree_units(B, L, H, D, e, b, LB, S):
     )
 
 
-def read_traffic(kernel: str, config: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{config}_traffic.md")
+def read_traffic(phase: str, config: str):
+    """HBM bytes per launch of `phase`'s main kernel from the committed rocprofv3 counter summary
+    (``profiles/traffic_<config>.md``, FETCH_SIZE/WRITE_SIZE calibrated by a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    m = re.search(r"traffic_bytes_per_launch\[" + re.escape(phase) + r"\]:\s*([0-9.eE+]+)", open(path).read())
     return float(m.group(1)) if m else None
 
 

@@ -174,6 +174,21 @@ __device__ __forceinline__ typename Mfma<E>::frag acc_operand(const f32x4 (&acc)
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// dst[0..4) = scale * v as E, one 8-byte (16-bit E) or 16-byte (float) store;
+// dst must be aligned to 4 elements.
+template <typename E>
+__device__ __forceinline__ void store4(E* dst, f32x4 v, float scale) {
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(4))) E v4;
+    v4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = (E)(v[r] * scale);
+    *(v4*)dst = o;
+  } else {
+    *(f32x4*)dst = v * scale;
+  }
+}
+
 template <typename E> __device__ __forceinline__ typename Mfma<E>::frag zero_frag() {
   typename Mfma<E>::frag r;
   if constexpr (Mfma<E>::KPL == 1) {
@@ -271,6 +286,26 @@ __device__ __forceinline__ void sum_rows8(float* acc, const E* rows, int64_t str
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] += (float)p[i];
   }
+}
+
+// ------------------------------------------------------- XCD placement ---
+// Workgroups are dispatched to the 8 XCDs of the chip round-robin by linear
+// id, and each XCD has its own L2.  xcd_bh_block maps linear id i to
+// (bh, beta) so that every leaf block of one (batch, head) runs on the same
+// XCD, in ascending beta (the heavy low blocks of causal runs first): the
+// rows that the blocks' pairs gather (queries, output gradients) then stay
+// in that XCD's L2.  Launch xcd_grid(nbh, nl) workgroups; ids with no work
+// get false.
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool xcd_bh_block(int i, int nbh, int nl, int& bh, int& beta) {
+  const int x = i % kXcds, j = i / kXcds;
+  const int r = j / nl;
+  beta = j - r * nl;
+  bh = r * kXcds + x;
+  return bh < nbh;
+}
+inline unsigned xcd_grid(int64_t nbh, int nl) {
+  return (unsigned)(((nbh + kXcds - 1) / kXcds) * kXcds * nl);
 }
 
 // ------------------------------------------------------------ reductions ---

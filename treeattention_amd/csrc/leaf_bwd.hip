@@ -73,9 +73,9 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   E* Kt = Zt + LBP * PS;   // [D][TS]    K^T (if kKt)
   int* ent_s = (int*)(Kt + (BT::kKt ? D * TS : 0));
 
-  // blocks of all heads interleave so the heavy low blocks of causal runs start first
-  const int nbh = a.B * a.H;
-  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
+  int bh, beta;
+  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
+  const int bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
@@ -201,10 +201,7 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
         else
           o = M::mma(ld_frag_perm_strided<E>(Ks + 16 * md + col, RS, ks, g), acc_operand<E>(pacc, ks), o);
       }
-      if (valid) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dqp[16 * md + 4 * g + r] = (E)(o[r] * a.scale);
-      }
+      if (valid) store4(dqp + 16 * md + 4 * g, o, a.scale);
     }
     __syncthreads();
 
@@ -271,8 +268,9 @@ __global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
   E* Pt = Gt + D * PS;     // [LBP][PS] (w P)^T
   E* Zt = Pt + LBP * PS;   // [LBP][PS] dz^T
 
-  const int nbh = a.B * a.H;
-  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
+  int bh, beta;
+  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
+  const int bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
@@ -384,10 +382,7 @@ __global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
 #pragma unroll
       for (int ks = 0; ks < LBP / M::K; ++ks)
         o = M::mma(ld_frag_perm(Kt + (16 * md + col) * TS, ks, g), acc_operand<E>(pacc, ks), o);
-      if (valid) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dqp[16 * md + 4 * g + r] = (E)(o[r] * a.scale);
-      }
+      if (valid) store4(dqp + 16 * md + 4 * g, o, a.scale);
     }
 
     __syncthreads();  // phase B of the previous tile is done with the staging buffers
@@ -491,7 +486,7 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.dq_part = ws + P.bws.dq_part;
   a.dv = dv;
   a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
-  const unsigned grid = (unsigned)(P.BH * P.geo.NL);
+  const unsigned grid = xcd_grid(P.BH, P.geo.NL);
   constexpr int smem8 = Bwd8Tile<D, LBP, (int)sizeof(E)>::bytes;
   if constexpr (LBP <= 64 && smem8 <= 160 * 1024 && (LBP / 16) * (D / 16) % 8 == 0) {
     hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd8_kernel<E, D, LBP>,

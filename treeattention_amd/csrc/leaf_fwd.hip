@@ -43,9 +43,9 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
   E* Ks = (E*)smem;         // [LBP][KS]
   E* Vt = Ks + LBP * KS;    // [D][VS]
 
-  // blocks of all heads interleave so the heavy low blocks of causal runs start first
-  const int nbh = a.B * a.H;
-  const int beta = blockIdx.x / nbh, bh = blockIdx.x - beta * nbh, bb = bh / a.H, h = bh - bb * a.H;
+  int bh, beta;
+  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
+  const int bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
   if (start >= end) return;
@@ -133,10 +133,7 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
       const E* vrow = Vt + (16 * md + col) * VS;
 #pragma unroll
       for (int ks = 0; ks < LBP / M::K; ++ks) o = M::mma(ld_frag_perm(vrow, ks, g), acc_operand<E>(sacc, ks), o);
-      if (valid) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[16 * md + 4 * g + r] = (E)(o[r] * f);
-      }
+      if (valid) store4(dst + 16 * md + 4 * g, o, f);
     }
   }
 }
@@ -200,7 +197,7 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3((unsigned)(P.BH * P.geo.NL)), dim3(256), smem, st, a);
+  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.geo.NL)), dim3(256), smem, st, a);
   const int64_t nqh = P.B * P.L * P.H;
   const int64_t nthr = nqh * (D / 8);
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,

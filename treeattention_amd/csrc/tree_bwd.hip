@@ -266,20 +266,30 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
     qa[qt].load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, g);
   }
   load_slots<E>(a, sm, bb, h, l0, nq, tid);
-  // Q^T for the summary-gradient product (rows past nq are zero fragments)
+  // Q^T for the summary-gradient product (rows past nq are zero fragments),
+  // transposed through LDS so every global store is a 16-byte row piece
+  {
+    E* qst = (E*)sm.Xs;  // [D][64]
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    if (qt != w) continue;
-    E* qt_out = (E*)a.qt + (int64_t)bh * D * a.Lp + l0 + 16 * qt + col;
+    for (int qt = 0; qt < 4; ++qt) {
+      if (qt != w) continue;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if constexpr (M::KPL == 1) {
-        qt_out[(int64_t)(ks * M::K + g) * a.Lp] = qa[qt].f[ks];
-      } else {
+      for (int ks = 0; ks < KS; ++ks) {
+        if constexpr (M::KPL == 1) {
+          qst[(ks * M::K + g) * kQueryTile + 16 * qt + col] = qa[qt].f[ks];
+        } else {
 #pragma unroll
-        for (int i = 0; i < M::KPL; ++i) qt_out[(int64_t)(ks * M::K + M::KPL * g + i) * a.Lp] = qa[qt].f[ks][i];
+          for (int i = 0; i < M::KPL; ++i) qst[(ks * M::K + M::KPL * g + i) * kQueryTile + 16 * qt + col] = qa[qt].f[ks][i];
+        }
       }
     }
+    __syncthreads();
+    E* qt_out = (E*)a.qt + (int64_t)bh * D * a.Lp + l0;
+    for (int e = tid; e < D * (kQueryTile / 8); e += 256) {
+      const int dd = e >> 3, q0 = (e & 7) * 8;
+      cp8(qt_out + (int64_t)dd * a.Lp + q0, qst + dd * kQueryTile + q0);
+    }
+    __syncthreads();
   }
 
   f32x4 dacc[NMD][4];
@@ -289,47 +299,94 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
     for (int qt = 0; qt < 4; ++qt) dacc[i][qt] = zero4();
   const E* sum_hi = (const E*)a.sum_hi;
   const E* sum_t = (const E*)a.sum_t;
-  for (int d = 0; d < T; ++d) {
-    const int lam = d + 1, lvl = G.pw[lam];
-    for (int c0 = 0; c0 < lvl; c0 += kChunk) {
-      const int ncols = min(kChunk, lvl - c0);
-      const int kcols = (ncols + 31) / 32 * 32;  // inside the level's zero padding
-      const int64_t r0 = (int64_t)bh * rows + G.off[lam] + c0;
-      // X^T tiles: rows of C (this wave's column tiles) against all 64 queries
-      for (int ct = w; ct < kcols / 16; ct += 4) {
-        const E* ar = sum_hi + (r0 + 16 * ct + col) * D + M::KPL * g;
-        F af[KS];
+
+  // Chunks (level d + 1, children [c0, c0 + kChunk)) in order.  Each wave
+  // holds the summary fragments of its logit tiles (tiles w, w + 4 of the
+  // chunk) and of its C^T rows (head-dim tiles w + 4i) for the whole chunk;
+  // the next chunk's are loaded as soon as the current ones are consumed, so
+  // their latency hides behind build_g and the other products.
+  constexpr int KT = kChunk / M::K;  // k-steps of the C^T G^T product per chunk
+  F af[2][KS];
+  F at[NMD][KT];
+  auto kcols_of = [&](int d, int c0) { return (min(kChunk, G.pw[d + 1] - c0) + 31) / 32 * 32; };
+  auto load_af = [&](int d, int c0) {
+    const int64_t r0 = (int64_t)bh * rows + G.off[d + 1] + c0;
+    const int kc = kcols_of(d, c0);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) af[ks] = ld_frag(ar + ks * M::K);
+    for (int j = 0; j < 2; ++j) {
+      const int ct = w + 4 * j;
+      if (ct < kc / 16) {
+        const E* ar = sum_hi + (r0 + 16 * ct + col) * D + M::KPL * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) af[j][ks] = ld_frag(ar + ks * M::K);
+      }
+    }
+  };
+  auto load_at = [&](int d, int c0) {
+    const int kc = kcols_of(d, c0);
+#pragma unroll
+    for (int i = 0; i < NMD; ++i) {
+      const int md = w + 4 * i;
+      if (md < D / 16) {
+        const E* ap = sum_t + ((int64_t)bh * D + 16 * md + col) * rows + G.off[d + 1] + c0 + M::KPL * g;
+#pragma unroll
+        for (int ks = 0; ks < KT; ++ks)
+          if (ks < kc / M::K) at[i][ks] = ld_frag(ap + ks * M::K);
+      }
+    }
+  };
+  int d = 0, c0 = 0;
+  if (T > 0) {
+    load_af(0, 0);
+    load_at(0, 0);
+  }
+  while (d < T) {
+    const int lam = d + 1, lvl = G.pw[lam];
+    const int ncols = min(kChunk, lvl - c0);
+    const int kcols = (ncols + 31) / 32 * 32;  // inside the level's zero padding
+    int nd = d, nc0 = c0 + kChunk;
+    if (nc0 >= lvl) {
+      nc0 = 0;
+      ++nd;
+    }
+    // X^T tiles: rows of C (this wave's column tiles) against all 64 queries
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ct = w + 4 * j;
+      if (ct < kcols / 16) {
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) {
           f32x4 c = zero4();
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) c = M::mma(af[ks], qa[qt].f[ks], c);
+          for (int ks = 0; ks < KS; ++ks) c = M::mma(af[j][ks], qa[qt].f[ks], c);
           *(f32x4*)(sm.Xs + (16 * qt + col) * kXS + 16 * ct + 4 * g) = c;
         }
       }
-      for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
-        const int r = e / (kcols / 8), c = (e - r * (kcols / 8)) * 8;
-        z8(sm.Gm + r * kGS + c);
-      }
-      __syncthreads();
-      build_g<E>(G, d, c0, ncols, S, a.lp, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
-      __syncthreads();
-      {
-        // G^T rows of the chunk (kcols covers the level's zero padding rows),
-        // eight queries per 16-byte store
-        E* gt = (E*)a.gt + ((int64_t)bh * rows + G.off[lam] + c0) * a.Lp + l0;
-        for (int e = tid; e < kcols * (kQueryTile / 8); e += 256) {
-          const int c = e >> 3, q0 = (e & 7) * 8;
-          E v8[8];
+    }
+    if (nd < T) load_af(nd, nc0);
+    for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
+      const int r = e / (kcols / 8), cc = (e - r * (kcols / 8)) * 8;
+      z8(sm.Gm + r * kGS + cc);
+    }
+    __syncthreads();
+    build_g<E>(G, d, c0, ncols, S, a.lp, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    __syncthreads();
+    {
+      // G^T rows of the chunk (kcols covers the level's zero padding rows),
+      // eight queries per 16-byte store
+      E* gt = (E*)a.gt + ((int64_t)bh * rows + G.off[lam] + c0) * a.Lp + l0;
+      for (int e = tid; e < kcols * (kQueryTile / 8); e += 256) {
+        const int cc = e >> 3, q0 = (e & 7) * 8;
+        E v8[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v8[i] = sm.Gm[(q0 + i) * kGS + c];
-          cp8(gt + (int64_t)c * a.Lp + q0, v8);
-        }
+        for (int i = 0; i < 8; ++i) v8[i] = sm.Gm[(q0 + i) * kGS + cc];
+        cp8(gt + (int64_t)cc * a.Lp + q0, v8);
       }
-      // dq^T += C^T G^T: A = C^T rows (head dims, from global), B = G rows (LDS)
-      for (int ks = 0; ks < kcols / M::K; ++ks) {
+    }
+    // dq^T += C^T G^T: A = C^T rows (head dims, registers), B = G rows (LDS)
+#pragma unroll
+    for (int ks = 0; ks < KT; ++ks) {
+      if (ks < kcols / M::K) {
         F bg[4];
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) bg[qt] = ld_frag(sm.Gm + (16 * qt + col) * kGS + ks * M::K + M::KPL * g);
@@ -337,15 +394,16 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
         for (int i = 0; i < NMD; ++i) {
           const int md = w + 4 * i;
           if (md < D / 16) {
-            const F at = ld_frag(sum_t + ((int64_t)bh * D + 16 * md + col) * rows + G.off[lam] + c0 + ks * M::K +
-                                 M::KPL * g);
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt) dacc[i][qt] = M::mma(at, bg[qt], dacc[i][qt]);
+            for (int qt = 0; qt < 4; ++qt) dacc[i][qt] = M::mma(at[i][ks], bg[qt], dacc[i][qt]);
           }
         }
       }
-      __syncthreads();
     }
+    if (nd < T) load_at(nd, nc0);
+    __syncthreads();
+    d = nd;
+    c0 = nc0;
   }
   // stage the tree dq as [q][d], add the leaf parts, write
   constexpr int SS = D + 4;
