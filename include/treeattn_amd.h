@@ -40,6 +40,19 @@ extern "C" {
 #define TA_BF16 1
 #define TA_F16 2
 
+/* causal semantics (ta_problem.causal) */
+#define TA_CAUSAL_NONE 0
+#define TA_CAUSAL_EXACT 1     /* bottom-right aligned (query t sees tokens <= t + N - L, needs
+                                 L <= N); sampling is restricted exactly to allowed leaf blocks */
+#define TA_CAUSAL_REFERENCE 2 /* the reference's causal stochastic mode (_tree_mha.py:125-268,
+                                 379-394): binary trees with leaf_block 1 (compat / node keys),
+                                 query t's boundary is leaf t; while every (batch, head, sample)
+                                 lane of a query is on the boundary path the decisions are
+                                 corrected by the boundary log-masses (fully allowed subtrees
+                                 weigh their leaf count), afterwards they are not; when
+                                 L > num_samples, queries t < num_samples get exact causal
+                                 attention (all leaves n <= t, softmax of the path log-probs) */
+
 /* how the per-node child summaries are built from `k` */
 #define TA_TREE_NATURAL 0  /* child summary = mean key of the child's subtree / 2 */
 #define TA_TREE_COMPAT 1   /* reference layout: in-order Haar of block means, read in heap order */
@@ -53,7 +66,7 @@ typedef struct ta_problem {
   int64_t branching;     /* b >= 2 */
   int64_t leaf_block;    /* LB >= 1 */
   int32_t tree_mode;     /* TA_TREE_* */
-  int32_t causal;        /* 0 or 1 (bottom-right aligned; L queries = L keys) */
+  int32_t causal;        /* TA_CAUSAL_* */
   int32_t dtype;         /* TA_F32 / TA_BF16 / TA_F16 */
   int32_t reserved;
   float scale;           /* leaf-block softmax scale */

@@ -65,6 +65,8 @@ def test_struct_layout_and_sizes():
     (dict(tree_mode=_lib.TA_TREE_COMPAT), ValueError),  # compat is binary
     (dict(causal=1, L=20000), ValueError),  # causal needs L <= N
     (dict(dtype=7), ValueError),
+    (dict(causal=2), ValueError),  # the reference causal mode needs the reference tree
+    (dict(causal=3), ValueError),
 ])
 def test_validation_errors(kw, exc):
     with pytest.raises(exc):

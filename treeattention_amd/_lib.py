@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(_PKG, "libtreeattn_amd.so")
 TA_OK = 0
 TA_F32, TA_BF16, TA_F16 = 0, 1, 2
 TA_TREE_NATURAL, TA_TREE_COMPAT, TA_TREE_NODEKEYS = 0, 1, 2
+TA_CAUSAL_NONE, TA_CAUSAL_EXACT, TA_CAUSAL_REFERENCE = 0, 1, 2
 
 TREE_MODES = {"natural": TA_TREE_NATURAL, "compat": TA_TREE_COMPAT, "nodekeys": TA_TREE_NODEKEYS}
 

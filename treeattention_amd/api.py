@@ -136,6 +136,7 @@ def tree_attention(
     max_logit: float = _DEFAULT_MAX_LOGIT,
     uniforms: torch.Tensor | None = None,
     return_weights: bool = False,
+    causal_mode: str = "auto",
 ):
     """Stochastic tree attention on ``(B, L, H, D)`` tensors.
 
@@ -144,11 +145,13 @@ def tree_attention(
     decisions, and the output is ``sum_s w_s softmax(scale q K_blk^T) V_blk``
     with ``w = softmax`` of the sampled path log-probabilities.  With
     ``branching=2, leaf_block=1, tree_mode="compat"`` this is the reference
-    adapter's stochastic non-causal computation (``baselines/treeattn_torch.py:48-90``).
+    adapter's stochastic computation (``baselines/treeattn_torch.py:48-90``),
+    causal included (``causal_mode="auto"`` selects the reference's causal
+    semantics on that tree; see ``TreeOptions``).
     """
     opts = TreeOptions(num_samples=int(num_samples), branching=int(branching), leaf_block=int(leaf_block),
-                       tree_mode=tree_mode, causal=bool(causal), scale=softmax_scale, max_logit=float(max_logit),
-                       seed=int(seed), layout="bshd")
+                       tree_mode=tree_mode, causal=bool(causal), causal_mode=causal_mode, scale=softmax_scale,
+                       max_logit=float(max_logit), seed=int(seed), layout="bshd")
     out, weights = TreeAttentionFunction.apply(q, k, v, opts, uniforms)
     return (out, weights) if return_weights else out
 

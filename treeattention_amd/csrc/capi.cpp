@@ -51,7 +51,8 @@ int make_plan(const ta_problem* p, Plan* P) {
   if (B < 1 || L < 1 || N < 1 || H < 1)
     return fail(TA_ERR_INVALID, "B, L, N, H must be >= 1 (got %lld, %lld, %lld, %lld)", (long long)B, (long long)L,
                 (long long)N, (long long)H);
-  if (p->causal && L > N) return fail(TA_ERR_INVALID, "causal needs L <= N (got L=%lld, N=%lld)", (long long)L, (long long)N);
+  if (p->causal == TA_CAUSAL_EXACT && L > N)
+    return fail(TA_ERR_INVALID, "causal needs L <= N (got L=%lld, N=%lld)", (long long)L, (long long)N);
   if (D != 32 && D != 64 && D != 96 && D != 128)
     return fail(TA_ERR_UNSUPPORTED, "head_dim must be one of 32, 64, 96, 128 (got %lld)", (long long)D);
   if (S < 1 || S > kMaxSamples)
@@ -68,7 +69,11 @@ int make_plan(const ta_problem* p, Plan* P) {
     return fail(TA_ERR_INVALID, "compat and node-key trees are binary (branching=%lld)", (long long)b);
   if (p->tree_mode == TA_TREE_NODEKEYS && LB != 1)
     return fail(TA_ERR_INVALID, "node-key trees have one leaf per position (leaf_block=%lld)", (long long)LB);
-  if (p->causal != 0 && p->causal != 1) return fail(TA_ERR_INVALID, "causal must be 0 or 1");
+  if (p->causal != TA_CAUSAL_NONE && p->causal != TA_CAUSAL_EXACT && p->causal != TA_CAUSAL_REFERENCE)
+    return fail(TA_ERR_INVALID, "causal must be TA_CAUSAL_NONE, _EXACT or _REFERENCE (got %d)", p->causal);
+  if (p->causal == TA_CAUSAL_REFERENCE && (b != 2 || LB != 1 || p->tree_mode == TA_TREE_NATURAL))
+    return fail(TA_ERR_INVALID, "the reference causal mode needs the reference tree: branching 2, leaf_block 1, "
+                                "compat or node-key summaries");
   if (!(p->max_logit > 0.f)) return fail(TA_ERR_INVALID, "max_logit must be > 0");
   const int64_t NL = N / LB;
   int T = 0;
@@ -133,6 +138,7 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.hist = r.take(P->BH * NL * P->nchunk * 4);
   P->rec.block_start = r.take(P->BH * (NL + 1) * 4);
   P->rec.order = r.take(P->BH * L * S * 4);
+  P->rec.dstar = r.take(p->causal == TA_CAUSAL_REFERENCE ? L * 4 : 0);
   P->rec.total = r.at;
   Carver f;
   P->fws.partial = f.take(BLHS * D * es);
@@ -146,8 +152,14 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->bws.qt = w.take(P->BH * D * P->Lp * es);
   P->bws.dsum_part = w.take(qsplit * P->BH * G.NS * D * 4);
   P->bws.dsum = w.take(P->BH * G.NS * D * 4);
+  const bool rc = p->causal == TA_CAUSAL_REFERENCE;
+  P->bws.rc_coef = w.take(rc ? B * L * H * T * 4 : 0);
+  P->bws.rc_rho = w.take(rc ? B * L * H * T * 4 : 0);
   P->bws.total = w.at;
 
+  if (rc && ref_sample_smem(*P) > 160 * 1024)
+    return fail(TA_ERR_UNSUPPORTED, "the reference causal mode keeps a query's B*H*S lanes in one workgroup; "
+                                    "B*H*S=%lld is too large", (long long)(P->BH * S));
   if (leaf_fwd_smem(*P) < 0 || leaf_bwd_smem(*P) < 0)
     return fail(TA_ERR_UNSUPPORTED, "leaf_block=%lld with head_dim=%lld in this dtype exceeds the 160 KiB LDS tile",
                 (long long)LB, (long long)D);

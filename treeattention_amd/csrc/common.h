@@ -308,6 +308,32 @@ inline unsigned xcd_grid(int64_t nbh, int nl) {
   return (unsigned)(((nbh + kXcds - 1) / kXcds) * kXcds * nl);
 }
 
+// ------------------------------------------------------ vector-ALU dots ---
+
+__device__ __forceinline__ float logsig(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }
+
+// q . c for one query row (E) and one float summary row, D a multiple of 8
+template <typename E>
+__device__ __forceinline__ float dot_row(const E* q, const float* c, int D) {
+  float acc = 0.f;
+  for (int i = 0; i < D; i += 8) {
+    float x[8];
+    if constexpr (sizeof(E) == 2) {
+      typedef __attribute__((ext_vector_type(8))) E v8;
+      const v8 v = *(const v8*)(q + i);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
+    } else {
+      const float4 a = *(const float4*)(q + i), b = *(const float4*)(q + i + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+    const float4 c0 = *(const float4*)(c + i), c1 = *(const float4*)(c + i + 4);
+    acc += x[0] * c0.x + x[1] * c0.y + x[2] * c0.z + x[3] * c0.w + x[4] * c1.x + x[5] * c1.y + x[6] * c1.z +
+           x[7] * c1.w;
+  }
+  return acc;
+}
+
 // ------------------------------------------------------------ reductions ---
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -367,6 +393,7 @@ struct RecordLayout {
   int64_t hist;        // int (BH, NL, nchunk): pair counts, then scanned offsets
   int64_t block_start; // int (BH, NL + 1)
   int64_t order;       // int (BH, L*S): (l*S + u) grouped by leaf block
+  int64_t dstar;       // int (L): reference causal mode: first uncorrected depth per query
   int64_t total;
 };
 
@@ -384,6 +411,8 @@ struct BwdWorkspaceLayout {
   int64_t qt;        // E (BH, D, Lp): queries transposed
   int64_t dsum_part; // float (qsplit, BH, NS, D)
   int64_t dsum;      // float (BH, NS, D)
+  int64_t rc_coef;   // float (B, L, H, T): reference causal mode, boundary-mass gradient scale
+  int64_t rc_rho;    // float (B, L, H, T): reference causal mode, on-path share of each boundary mass
   int64_t total;
 };
 

@@ -26,6 +26,9 @@ hipError_t launch_fill_uniforms(uint64_t seed, int64_t n, float* out, hipStream_
 // sample.hip
 hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
                          float* weights, char* rec, hipStream_t st);
+// sample_ref.hip (reference causal mode)
+hipError_t launch_ref_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
+                             float* weights, char* rec, hipStream_t st);
 // bucket.hip
 hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st);
 // leaf_fwd.hip
@@ -41,6 +44,7 @@ hipError_t launch_tree_bwd(const Plan& P, const void* q, const float* weights, c
 // Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
 // variant fits in 160 KiB.
 int leaf_fwd_smem(const Plan& P);
+int ref_sample_smem(const Plan& P);
 int leaf_bwd_smem(const Plan& P);
 
 inline int padded_keys(int LB) { return LB <= 32 ? 32 : (LB <= 64 ? 64 : 128); }

@@ -467,7 +467,7 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.S = (int)P.S;
   a.NL = P.geo.NL;
   a.LB = P.geo.LB;
-  a.causal = P.p.causal;
+  a.causal = P.p.causal == TA_CAUSAL_EXACT;
   a.scale = P.p.scale;
   a.scale_log2 = P.p.scale * 1.4426950408889634f;
   const bool nodekeys = P.p.tree_mode == TA_TREE_NODEKEYS;

@@ -475,7 +475,7 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.L = (int)P.L;
   a.H = (int)P.H;
   a.S = (int)P.S;
-  a.causal = P.p.causal;
+  a.causal = P.p.causal == TA_CAUSAL_EXACT;
   a.coff = (int)(P.N - P.L);
   a.maxhalf = 0.5f * P.p.max_logit;
   a.q = q;
@@ -532,6 +532,7 @@ static hipError_t sample_d(const Plan& P, const void* q, const float* U, uint64_
 
 hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
                          char* rec, hipStream_t st) {
+  if (P.p.causal == TA_CAUSAL_REFERENCE) return launch_ref_sample(P, q, U, seed, weights, rec, st);
   switch (P.p.dtype) {
     case TA_F32: return sample_d<float>(P, q, U, seed, weights, rec, st);
     case TA_BF16: return sample_d<bf16>(P, q, U, seed, weights, rec, st);

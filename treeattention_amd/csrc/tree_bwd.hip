@@ -54,6 +54,13 @@ struct TreeArgs {
   int64_t ksb, ksl, ksh;
   int qsplit;
   int lp;  // log2 of S rounded up to a power of two
+  // reference causal mode
+  int refc, t0;           // t0: first sampled query row (queries below it are the exact head)
+  int64_t nqh;            // B * L * H
+  const float* sum32;     // float (BH, NS, D) summaries
+  const int* dstar;       // (L) first uncorrected depth per query
+  float* rc_coef;         // (B, L, H, T)
+  float* rc_rho;          // (B, L, H, T)
 };
 
 template <typename E>
@@ -94,6 +101,67 @@ __global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__
   float tot = w * dt;
   for (int o = 1; o < P; o <<= 1) tot += __shfl_xor(tot, o, 64);
   if (act) dl[qh * S + u] = w * (dt - tot);
+}
+
+// Reference causal mode (_tree_mha.py:198-262): a sampled query row t whose
+// lanes were not all on the boundary path from depth D* on (D* < T) gives the
+// samples still on the path at D* the log-mass M_{D*} in their log-prob, and
+// M_{D*} depends on the boundary logits of depths d >= D*:
+//   M_d = logsumexp(M_{d+1} + logsig(on_d), m_off,d + logsig(off_d)),  M_T = 0,
+//   dM_{D*}/dx_j(d) = Gamma_d (rho_j - p_j),   Gamma_d = prod_{D* <= e < d} pi_e,
+// with p the child probabilities of boundary node d, rho_on = pi_d =
+// exp(M_{d+1} + logsig(on_d) - M_d), rho_off = 1 - pi_d.  One thread per
+// (batch, position, head) writes coef_d = A_on Gamma_d (A_on = the summed dl
+// of the slots below the depth-D* boundary node) and rho_d = pi_d for
+// d >= D*, zeros elsewhere; tree_dq adds coef_d (rho_j - p_j) to G.  The
+// common -M_0 of every sample of a row has no gradient (sum_s dlogp_s = 0).
+template <typename E>
+__global__ __launch_bounds__(256) void ref_causal_grad_kernel(TreeArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int H = a.H, L = a.L, T = a.geo.T, D = a.D;
+  if (gid >= a.nqh) return;
+  const int h = (int)(gid % H);
+  const int64_t bl = gid / H;
+  const int t = (int)(bl % L), bb = (int)(bl / L);
+  float* cf = a.rc_coef + gid * T;
+  float* rh = a.rc_rho + gid * T;
+  for (int d = 0; d < T; ++d) {
+    cf[d] = 0.f;
+    rh[d] = 0.f;
+  }
+  if (t < a.t0) return;
+  const int ds = a.dstar[t];
+  if (ds >= T) return;
+  const int c = t, bh = bb * H + h;
+  const E* qr = (const E*)a.q + bb * a.qsb + (int64_t)t * a.qsl + h * a.qsh;
+  // bottom-up masses and pi_d for d = T-1 .. D*
+  float m = 0.f;
+  for (int d = T - 1; d >= ds; --d) {
+    const float* crow = a.sum32 + ((int64_t)bh * a.geo.NS + a.geo.off[d + 1] + 2 * (c >> (T - d))) * D;
+    const float x = 2.f * dot_row(qr, crow, D);
+    const int dir = (c >> (T - 1 - d)) & 1;
+    const float on = dir ? logsig(-x) : logsig(x), off = dir ? logsig(x) : logsig(-x);
+    const float a0 = m + on;
+    float md = a0;
+    if (dir) {
+      const float a1 = logf((float)(1 << (T - 1 - d))) + off;
+      const float mx = fmaxf(a0, a1);
+      md = mx + logf(expf(a0 - mx) + expf(a1 - mx));
+    }
+    rh[d] = expf(a0 - md);
+    m = md;
+  }
+  // A_on: slots below the depth-D* boundary node
+  const int node = c >> (T - ds);
+  const int cnt = a.slot_count[gid];
+  float A = 0.f;
+  for (int u = 0; u < cnt; ++u)
+    if ((a.slot_leaf[gid * a.S + u] >> (T - ds)) == node) A += a.dl[gid * a.S + u];
+  float gam = 1.f;
+  for (int d = ds; d < T; ++d) {
+    cf[d] = A * gam;
+    gam *= rh[d];
+  }
 }
 
 // Query tile of the dq kernel in LDS: child logits of the current chunk, G of
@@ -371,6 +439,25 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
     __syncthreads();
     build_g<E>(G, d, c0, ncols, S, a.lp, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
     __syncthreads();
+    if (a.refc) {
+      // boundary-mass gradient of the reference causal mode (ref_causal_grad_kernel)
+      if (tid < nq) {
+        const int t = l0 + tid;
+        const int64_t qh = ((int64_t)bb * a.L + t) * a.H + h;
+        const float cf = a.rc_coef[qh * T + d];
+        const int base = 2 * (t >> (T - d)) - c0;  // the boundary node's left child
+        if (cf != 0.f && base >= 0 && base < ncols) {
+          const float xl = sm.Xs[tid * kXS + base], xr = sm.Xs[tid * kXS + base + 1];
+          const float pl = 1.f / (1.f + __expf(xr - xl));
+          const float rho = a.rc_rho[qh * T + d];
+          const float rl = ((t >> (T - 1 - d)) & 1) ? 1.f - rho : rho;
+          E* gr = sm.Gm + tid * kGS + base;
+          gr[0] = (E)((float)gr[0] + cf * (rl - pl));
+          gr[1] = (E)((float)gr[1] + cf * (pl - rl));
+        }
+      }
+      __syncthreads();
+    }
     {
       // G^T rows of the chunk (kcols covers the level's zero padding rows),
       // eight queries per 16-byte store
@@ -573,7 +660,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.H = (int)P.H;
   a.S = (int)P.S;
   a.D = D;
-  a.causal = P.p.causal;
+  a.causal = P.p.causal == TA_CAUSAL_EXACT;
   a.mode = P.p.tree_mode;
   a.maxhalf = 0.5f * P.p.max_logit;
   a.q = q;
@@ -598,12 +685,21 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.qsplit = P.qsplit;
   a.lp = 0;
   while ((1 << a.lp) < P.S) ++a.lp;
+  a.refc = P.p.causal == TA_CAUSAL_REFERENCE;
+  a.t0 = P.L > P.S ? (int)P.S : 0;
+  a.nqh = P.B * P.L * P.H;
+  a.sum32 = (const float*)(rec + P.rec.summaries);
+  a.dstar = (const int*)(rec + P.rec.dstar);
+  a.rc_coef = (float*)(ws + P.bws.rc_coef);
+  a.rc_rho = (float*)(ws + P.bws.rc_rho);
 
   const int64_t nqh = P.B * P.L * P.H;
   int pw2 = 1;
   while (pw2 < P.S) pw2 <<= 1;
   hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
                      a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh);
+  if (a.refc)
+    hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
   const int smem_q = tree_smem(P);
   hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
   if (e != hipSuccess) return e;

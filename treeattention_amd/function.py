@@ -12,6 +12,7 @@ reference (``_autograd.py:703``).
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import math
 from dataclasses import dataclass
 
@@ -32,8 +33,19 @@ class TreeOptions:
       leaf-block means, read in heap order), ``"natural"`` (child summary =
       half the mean key of the child's subtree) or ``"nodekeys"`` (``k`` holds
       the heap-ordered node keys, the op-level reference API).
-    * ``causal``: bottom-right aligned mask; sampling is restricted exactly to
-      allowed leaf blocks.
+    * ``causal``: causal attention, with ``causal_mode``:
+
+      - ``"reference"``: the reference's causal stochastic mode
+        (``_tree_mha.py:125-268,379-394``), for the reference tree only
+        (``branching=2, leaf_block=1``, compat or node-key summaries): query
+        ``t`` has boundary leaf ``t``; decisions are corrected by the boundary
+        log-masses while every (batch, head, sample) lane of the query is on
+        the boundary path, plain afterwards; with ``L > num_samples`` the first
+        ``num_samples`` queries get exact causal attention;
+      - ``"exact"``: bottom-right aligned mask with sampling restricted exactly
+        to the allowed leaf blocks (any tree);
+      - ``"auto"`` (default): ``"reference"`` on the reference tree, else
+        ``"exact"``.
     * ``scale``: leaf-block softmax scale (``None`` -> ``1/sqrt(D)``).
     * ``max_logit``: child logits are clamped to ``+-max_logit/2``.
     * ``seed``: counter-RNG key for the Gumbel uniforms when no explicit
@@ -46,6 +58,7 @@ class TreeOptions:
     leaf_block: int = 1
     tree_mode: str = "compat"
     causal: bool = False
+    causal_mode: str = "auto"
     scale: float | None = None
     max_logit: float = 1e3
     seed: int = 0
@@ -67,6 +80,21 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     if t.stride(-1) != 1 or any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
         t = t.contiguous()
     return t
+
+
+_HEAD_DIMS = (32, 64, 96, 128)
+
+
+def _pad_heads(q, k, v, opts: TreeOptions):
+    """Zero-pads the head dim to the next size the kernels implement (dots and
+    value rows are unchanged by zero columns); the softmax scale keeps the true D."""
+    D = q.shape[-1]
+    if D > 128 or D % 8:
+        raise NotImplementedError(f"head_dim must be a multiple of 8 up to 128 (got {D})")
+    Dp = next(x for x in _HEAD_DIMS if x >= D)
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dp - D))  # noqa: E731
+    scale = opts.scale if opts.scale is not None else 1.0 / math.sqrt(D)
+    return pad(q), pad(k), pad(v), dataclasses.replace(opts, scale=scale)
 
 
 def make_problem(q, k, v, opts: TreeOptions) -> _lib.Problem:
@@ -92,7 +120,7 @@ def make_problem(q, k, v, opts: TreeOptions) -> _lib.Problem:
     p.branching = opts.branching
     p.leaf_block = opts.leaf_block
     p.tree_mode = _lib.TREE_MODES[opts.tree_mode]
-    p.causal = int(bool(opts.causal))
+    p.causal = _causal_code(opts)
     p.dtype = _DTYPES[q.dtype]
     p.scale = float(opts.scale) if opts.scale is not None else 1.0 / math.sqrt(D)
     p.max_logit = float(opts.max_logit)
@@ -102,6 +130,22 @@ def make_problem(q, k, v, opts: TreeOptions) -> _lib.Problem:
     p.o_strides[:] = _strides(q, opts.layout)
     p.g_strides[:] = _strides(q, opts.layout)
     return p
+
+
+def reference_tree(opts: TreeOptions) -> bool:
+    """True for the reference's tree: binary, one token per leaf, Haar / node keys."""
+    return opts.branching == 2 and opts.leaf_block == 1 and opts.tree_mode in ("compat", "nodekeys")
+
+
+def _causal_code(opts: TreeOptions) -> int:
+    if not opts.causal:
+        return _lib.TA_CAUSAL_NONE
+    mode = opts.causal_mode
+    if mode == "auto":
+        mode = "reference" if reference_tree(opts) else "exact"
+    if mode not in ("reference", "exact"):
+        raise ValueError(f"causal_mode must be 'auto', 'reference' or 'exact' (got {opts.causal_mode!r})")
+    return _lib.TA_CAUSAL_REFERENCE if mode == "reference" else _lib.TA_CAUSAL_EXACT
 
 
 def _weights_like(q: torch.Tensor, S: int, layout: str) -> tuple[torch.Tensor, tuple[int, int, int]]:
@@ -120,6 +164,11 @@ def _stream(dev: torch.device) -> int:
 def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = None):
     """Forward only: returns ``(out, weights, record)``."""
     lib = _lib.load()
+    D = q.shape[-1]
+    if D not in _HEAD_DIMS:
+        q, k, v, opts = _pad_heads(q, k, v, opts)
+        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+        return out[..., :D], weights, record
     q, k, v = _prep(q), _prep(k), _prep(v)
     prob = make_problem(q, k, v, opts)
     rec_b, fws_b, _ = _lib.byte_sizes(prob)
@@ -147,6 +196,12 @@ def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = Non
 def tree_backward(q, k, v, weights, record, grad_out, opts: TreeOptions):
     """Backward from a forward record: returns ``(dq, dk, dv)``."""
     lib = _lib.load()
+    D = q.shape[-1]
+    if D not in _HEAD_DIMS:
+        q, k, v, opts = _pad_heads(q, k, v, opts)
+        grad_out = torch.nn.functional.pad(grad_out, (0, q.shape[-1] - D))
+        dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, opts)
+        return dq[..., :D], dk[..., :D], dv[..., :D]
     q, k, v = _prep(q), _prep(k), _prep(v)
     grad_out = _prep(grad_out)
     prob = make_problem(q, k, v, opts)
@@ -214,6 +269,10 @@ class StochasticTreeAttention(torch.autograd.Function):
         out, weights, record = tree_forward(q, k, v, opts, uniforms)
         ctx.save_for_backward(q, k, v, weights, record)
         ctx.opts = opts
+        if is_causal and q.shape[0] > num_samples:
+            # hybrid: the first num_samples queries are exact; the reference returns the
+            # sample weights of the other rows only (_tree_mha.py:379-413)
+            weights = weights[num_samples:]
         ctx.mark_non_differentiable(weights)
         return out, weights
 
@@ -233,7 +292,10 @@ class StochasticTreeAttention(torch.autograd.Function):
 
 
 def record_views(q, k, v, opts: TreeOptions, record: torch.Tensor):
-    """``(leaves (B,L,H,S) int32, summaries (B*H, NS, D) float32)`` views of a record."""
+    """``(leaves (B,L,H,S) int32, summaries (B*H, NS, D) float32)`` views of a record
+    (``D`` padded to a kernel head size where the forward padded it)."""
+    if q.shape[-1] not in _HEAD_DIMS:
+        q, k, v, opts = _pad_heads(q, k, v, opts)
     q, k, v = _prep(q), _prep(k), _prep(v)
     prob = make_problem(q, k, v, opts)
     lo = _lib.record_offset(prob, _lib.TA_REC_LEAVES)
