@@ -239,34 +239,62 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   }
 }
 
-// Eight-wave variant: 128-pair tiles.  Phase A (each wave, its 16 pairs):
-// query and output-gradient rows come straight from global memory into MFMA
-// fragments (the next tile's are loaded while this one computes), then P,
-// delta, dz and the pair's dq.  Phase B (all waves): dV and dK over the 128
-// pairs from transposed LDS copies, every fragment a contiguous 16-byte read.
-template <int D, int LBP, int ES>
-struct Bwd8Tile {
+// Eight-wave variant for 16-bit inputs: 128-pair tiles.  Phase A (each wave,
+// its 16 pairs): query and output-gradient rows come straight from global
+// memory into MFMA fragments (the next tile's are loaded while this one
+// computes), then P, delta, dz and the pair's dq; the wave then stores its
+// rows of Q, dout, wP and dz into row-major LDS tiles with 16- and 8-byte
+// writes.  Phase B (all waves, 2x2 output tiles each): dV += (wP)^T dout and
+// dK += dz^T Q over the tile's 128 pairs.  The MFMA operands of phase B and
+// K^T of the dq product are read with ds_read_b64_tr_b16, gfx950's transposing
+// LDS read: within each group of 16 lanes, lane i receives element i%4 of the
+// 8-byte slots of lanes 4r + i/4 (r = 0..3), so pointing lane j of a group at
+// row k0 + j/4, columns 4(j%4).. of a row-major [k][n] tile gives lane i the
+// four values [k0..k0+3][n = i] -- a k-contiguous operand column.  Row strides
+// are padded by 16 elements so every 16-lane group touches distinct banks.
+template <int D, int LBP>
+struct BwdTrTile {
   static constexpr int QT = 128;
-  static constexpr int RS = D + 8, TS = LBP + 8, PS = QT + 8;
-  static constexpr int bytes = (2 * LBP * RS + D * TS + 2 * D * PS + 2 * LBP * PS) * ES;
+  static constexpr int RS = D + 16, PS = LBP + 16;
+  static constexpr int bytes = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
 };
 
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+
+// Four 16-bit values [k0..k0+3][n] of a row-major LDS tile X (row stride rs
+// elements) for lane i = n - n0 of each 16-lane group; `row` = k0 + (lane%16)/4,
+// `col` = n0 + 4 (lane % 4).
+template <typename E>
+__device__ __forceinline__ s16x4 tr_read(const E* X, int rs, int row, int col) {
+  typedef __attribute__((address_space(3))) s16x4* lp;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(X + row * rs + col));
+}
+
+// An MFMA operand fragment of k = 8 values: rows k0a..k0a+3 then k0b..k0b+3.
+template <typename E>
+__device__ __forceinline__ typename Mfma<E>::frag tr_frag(const E* X, int rs, int k0a, int k0b, int n0, int lane) {
+  const int j = lane & 15;
+  const s16x4 lo = tr_read(X, rs, k0a + (j >> 2), n0 + 4 * (j & 3));
+  const s16x4 hi = tr_read(X, rs, k0b + (j >> 2), n0 + 4 * (j & 3));
+  typedef __attribute__((ext_vector_type(8))) short s16x8;
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Mfma<E>::frag, v);
+}
+
 template <typename E, int D, int LBP>
-__global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
+__global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
+  static_assert(sizeof(E) == 2, "16-bit inputs");
   using M = Mfma<E>;
-  using BT = Bwd8Tile<D, LBP, (int)sizeof(E)>;
-  constexpr int QT = BT::QT, RS = BT::RS, TS = BT::TS, PS = BT::PS;
+  using BT = BwdTrTile<D, LBP>;
+  constexpr int QT = BT::QT, RS = BT::RS, PS = BT::PS;
   constexpr int NW = 8;
-  constexpr int NT = (LBP / 16) * (D / 16) / NW;  // dV / dK tiles per wave
-  static_assert(NT >= 1 && (LBP / 16) * (D / 16) % NW == 0, "tile split");
   extern __shared__ __align__(16) char smem[];
   E* Ks = (E*)smem;        // [LBP][RS]
   E* Vs = Ks + LBP * RS;   // [LBP][RS]
-  E* Kt = Vs + LBP * RS;   // [D][TS]
-  E* Qt = Kt + D * TS;     // [D][PS]   Q^T of the tile
-  E* Gt = Qt + D * PS;     // [D][PS]   dout^T of the tile
-  E* Pt = Gt + D * PS;     // [LBP][PS] (w P)^T
-  E* Zt = Pt + LBP * PS;   // [LBP][PS] dz^T
+  E* Qs = Vs + LBP * RS;   // [QT][RS]  Q rows of the tile
+  E* Gs = Qs + QT * RS;    // [QT][RS]  dout rows of the tile
+  E* Ps = Gs + QT * RS;    // [QT][PS]  w P rows
+  E* Zs = Ps + QT * PS;    // [QT][PS]  dz rows
 
   int bh, beta;
   if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
@@ -288,14 +316,19 @@ __global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
     else zero8e(Ks + key * RS + c);
     if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
     else zero8e(Vs + key * RS + c);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) Kt[(c + i) * TS + key] = Ks[key * RS + c + i];
   }
   __syncthreads();
 
-  f32x4 dvacc[NT], dkacc[NT];
+  // phase B output tiles of this wave: keys 16 mk0 .. +31, dims 16 nd0 .. +31
+  constexpr int MKW = LBP / 32;                     // key-tile pairs
+  constexpr int NDW = D / 32;                       // dim-tile pairs
+  constexpr int NBLK = MKW * NDW;                   // 2x2 blocks per output
+  constexpr int NB = (NBLK + NW - 1) / NW;          // blocks per wave
+  f32x4 dvacc[NB][4], dkacc[NB][4];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) { dvacc[t] = zero4(); dkacc[t] = zero4(); }
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { dvacc[i][t] = zero4(); dkacc[i][t] = zero4(); }
 
   const int* ord = a.order + (int64_t)bh * LS;
   const int pcol = 16 * w + col;  // this lane's pair column within the tile
@@ -375,72 +408,91 @@ __global__ __launch_bounds__(512) void leaf_bwd8_kernel(LeafBwdArgs a) {
       for (int r = 0; r < 4; ++r) pacc[mt][r] = wt * sacc[mt][r] * (pacc[mt][r] - delta);
     if (valid && g == 0) a.delta[qh * S + u] = delta;
 
+    // dq_pair^T = K^T dz^T: K^T fragments read transposed from Ks in the
+    // accumulator's key order (keys 32ks + 4g.. and 32ks + 16 + 4g..)
     E* dqp = (E*)a.dq_part + (qh * S + u) * D;
 #pragma unroll
     for (int md = 0; md < D / 16; ++md) {
       f32x4 o = zero4();
 #pragma unroll
       for (int ks = 0; ks < LBP / M::K; ++ks)
-        o = M::mma(ld_frag_perm(Kt + (16 * md + col) * TS, ks, g), acc_operand<E>(pacc, ks), o);
+        o = M::mma(tr_frag(Ks, RS, 32 * ks + 4 * g, 32 * ks + 16 + 4 * g, 16 * md, lane), acc_operand<E>(pacc, ks), o);
       if (valid) store4(dqp + 16 * md + 4 * g, o, a.scale);
     }
 
-    __syncthreads();  // phase B of the previous tile is done with the staging buffers
+    __syncthreads();  // phase B of the previous tile is done with the staging tiles
+    {
+      E* pr = Ps + pcol * PS + 4 * g;
+      E* zr = Zs + pcol * PS + 4 * g;
 #pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt)
+      for (int mt = 0; mt < LBP / 16; ++mt) {
+        typedef __attribute__((ext_vector_type(4))) E e4;
+        e4 pv, zv;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = 16 * mt + 4 * g + r;
-        Pt[key * PS + pcol] = (E)(wt * sacc[mt][r]);
-        Zt[key * PS + pcol] = (E)pacc[mt][r];
+        for (int r = 0; r < 4; ++r) {
+          pv[r] = (E)(wt * sacc[mt][r]);
+          zv[r] = (E)pacc[mt][r];
+        }
+        *(e4*)(pr + 16 * mt) = pv;
+        *(e4*)(zr + 16 * mt) = zv;
       }
 #pragma unroll
-    for (int ks = 0; ks < D / M::K; ++ks) {
-      if constexpr (M::KPL == 1) {
-        Qt[(ks * M::K + g) * PS + pcol] = qc.f[ks];
-        Gt[(ks * M::K + g) * PS + pcol] = gc.f[ks];
-      } else {
-#pragma unroll
-        for (int i = 0; i < M::KPL; ++i) {
-          Qt[(ks * M::K + M::KPL * g + i) * PS + pcol] = qc.f[ks][i];
-          Gt[(ks * M::K + M::KPL * g + i) * PS + pcol] = gc.f[ks][i];
-        }
+      for (int ks = 0; ks < D / M::K; ++ks) {
+        *(typename M::frag*)(Qs + pcol * RS + ks * M::K + M::KPL * g) = qc.f[ks];
+        *(typename M::frag*)(Gs + pcol * RS + ks * M::K + M::KPL * g) = gc.f[ks];
       }
     }
     __syncthreads();
 
-    // ---- phase B: dV, dK over the tile's 128 pairs
+    // ---- phase B: dV, dK over the tile's 128 pairs, 2x2 output tiles per wave
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tile = w + NW * t;
-      const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
-      const E* pa = Pt + (16 * mk + col) * PS + M::KPL * g;
-      const E* za = Zt + (16 * mk + col) * PS + M::KPL * g;
-      const E* gb = Gt + (16 * nd + col) * PS + M::KPL * g;
-      const E* qb = Qt + (16 * nd + col) * PS + M::KPL * g;
+    for (int i = 0; i < NB; ++i) {
+      const int blk = w + NW * i;
+      if (blk < NBLK) {
+        const int mk0 = 2 * (blk / NDW), nd0 = 2 * (blk % NDW);
 #pragma unroll
-      for (int ks = 0; ks < QT / M::K; ++ks) {
-        dvacc[t] = M::mma(ld_frag(pa + ks * M::K), ld_frag(gb + ks * M::K), dvacc[t]);
-        dkacc[t] = M::mma(ld_frag(za + ks * M::K), ld_frag(qb + ks * M::K), dkacc[t]);
+        for (int ks = 0; ks < QT / M::K; ++ks) {
+          const int ka = 32 * ks + 8 * g, kb = ka + 4;
+          typename M::frag pa[2], za[2], gb[2], qb[2];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            pa[x] = tr_frag(Ps, PS, ka, kb, 16 * (mk0 + x), lane);
+            za[x] = tr_frag(Zs, PS, ka, kb, 16 * (mk0 + x), lane);
+            gb[x] = tr_frag(Gs, RS, ka, kb, 16 * (nd0 + x), lane);
+            qb[x] = tr_frag(Qs, RS, ka, kb, 16 * (nd0 + x), lane);
+          }
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) {
+              dvacc[i][2 * x + y] = M::mma(pa[x], gb[y], dvacc[i][2 * x + y]);
+              dkacc[i][2 * x + y] = M::mma(za[x], qb[y], dkacc[i][2 * x + y]);
+            }
+        }
       }
     }
   }
 
   E* dv = (E*)a.dv;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int tile = w + NW * t;
-    const int mk = tile / (D / 16), nd = tile - mk * (D / 16);
+  for (int i = 0; i < NB; ++i) {
+    const int blk = w + NW * i;
+    if (blk >= NBLK) continue;
+    const int mk0 = 2 * (blk / NDW), nd0 = 2 * (blk % NDW);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = 16 * mk + 4 * g + r;
-      if (key < LB) {
-        const int64_t tok = (int64_t)beta * LB + key;
-        const int d = 16 * nd + col;
-        dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[t][r];
-        if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[t][r] * a.scale;
-      }
-    }
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * (mk0 + x) + 4 * g + r;
+          if (key < LB) {
+            const int64_t tok = (int64_t)beta * LB + key;
+            const int d = 16 * (nd0 + y) + col;
+            dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[i][2 * x + y][r];
+            if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[i][2 * x + y][r] * a.scale;
+          }
+        }
   }
 }
 
@@ -487,12 +539,12 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.dv = dv;
   a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
   const unsigned grid = xcd_grid(P.BH, P.geo.NL);
-  constexpr int smem8 = Bwd8Tile<D, LBP, (int)sizeof(E)>::bytes;
-  if constexpr (LBP <= 64 && smem8 <= 160 * 1024 && (LBP / 16) * (D / 16) % 8 == 0) {
-    hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd8_kernel<E, D, LBP>,
+  constexpr int smem8 = BwdTrTile<D, LBP>::bytes;
+  if constexpr (sizeof(E) == 2 && LBP <= 64 && LBP >= 32 && smem8 <= 160 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_tr_kernel<E, D, LBP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem8);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((leaf_bwd8_kernel<E, D, LBP>), dim3(grid), dim3(512), smem8, st, a);
+    hipLaunchKernelGGL((leaf_bwd_tr_kernel<E, D, LBP>), dim3(grid), dim3(512), smem8, st, a);
   } else {
     const int smem = bwd_smem_t<E, D, LBP>();
     hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,
