@@ -112,14 +112,15 @@ int make_plan(const ta_problem* p, Plan* P) {
   if ((int64_t)NL * P->nchunk * P->BH > ((int64_t)1 << 29))
     return fail(TA_ERR_UNSUPPORTED, "too many leaf blocks x query chunks for the bucket table (NL=%lld)",
                 (long long)NL);
-  // summary gradient: 64-row tiles of the summaries, queries split so the
-  // product has a few thousand workgroups
+  // summary gradient: chunks of 384 summary rows; queries split into blocks of
+  // 32 so the product has about 512 workgroups (two per CU)
   const int64_t qtiles = (L + kQueryTile - 1) / kQueryTile;
   P->Lp = qtiles * kQueryTile;
-  const int64_t rowtiles = (G.NS + 63) / 64;
-  int64_t qsplit = rowtiles > 0 ? (4096 + rowtiles * P->BH - 1) / (rowtiles * P->BH) : 1;
+  const int64_t rowchunks = (G.NS / 16 + 23) / 24;
+  const int64_t kblocks = P->Lp / 32;
+  int64_t qsplit = (512 + rowchunks * P->BH - 1) / (rowchunks * P->BH);
   if (qsplit < 1) qsplit = 1;
-  if (qsplit > qtiles) qsplit = qtiles;
+  if (qsplit > kblocks) qsplit = kblocks;
   P->qsplit = (int)qsplit;
 
   const int64_t BLHS = B * L * H * S;

@@ -53,6 +53,7 @@ struct TreeArgs {
   void* dk;
   int64_t ksb, ksl, ksh;
   int qsplit;
+  int BHn;  // B * H
   int lp;  // log2 of S rounded up to a power of two
   // reference causal mode
   int refc, t0;           // t0: first sampled query row (queries below it are the exact head)
@@ -521,52 +522,109 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
 }
 
 // dC partial of one query split: dsum_part[split][bh][r][:] = sum over the
-// split's queries of G^T[r][q] Q[q][:].  Both operands are stored with the
-// queries contiguous, so every fragment is one contiguous load from global
-// memory.  grid (ceil(NS/64), BH, qsplit); wave w owns rows 16w..16w+15 of
-// the workgroup's 64 (NS is a multiple of 32, so a wave is in or out whole).
+// split's queries of G^T[r][q] Q[q][:].  grid (row chunks, qsplit, BH), eight
+// waves; a row chunk is 8 * kDcRows row tiles of 16 summary rows and wave w
+// owns tiles w, w + 8, ... of it for every head dim.  Per block of 32 queries
+// the Q^T block is staged once in LDS (double-buffered: the next block's
+// global loads are in flight while the current one is multiplied) and every
+// G^T row is read once, straight from global memory into MFMA fragments.
+constexpr int kDcRows = 3;   // row tiles per wave
+constexpr int kDcKB = 32;    // queries per staged block
+
 template <typename E, int D>
-__global__ __launch_bounds__(256) void tree_dc_kernel(TreeArgs a) {
+__global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   using M = Mfma<E>;
   using F = typename M::frag;
-  const int bh = blockIdx.y, split = blockIdx.z;
+  constexpr int KS = kDcKB / M::K;           // MFMA k-steps per block
+  constexpr int QS = kDcKB + 8;              // padded LDS row stride (elements)
+  constexpr int NDT = D / 16;
+  constexpr int NLD = D * (kDcKB / 8);       // 8-element pieces of a Q^T block
+  constexpr int PER = (NLD + 511) / 512;     // pieces per thread
+  __shared__ __align__(16) E qs[2][D * QS];
+  const int chunk = blockIdx.x, split = blockIdx.y, bh = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
-  const int rows = a.geo.NS;
-  const int r0 = 64 * blockIdx.x + 16 * w;
-  if (r0 >= rows) return;
+  const int rows = a.geo.NS, ntile = rows / 16;
   const int64_t Lp = a.Lp;
-  const int64_t per = ((Lp / kQueryTile + a.qsplit - 1) / a.qsplit) * kQueryTile;
+  const int64_t per = ((Lp / kDcKB + a.qsplit - 1) / a.qsplit) * kDcKB;
   const int64_t k0 = (int64_t)split * per, k1 = min(Lp, k0 + per);
-  const E* ap = (const E*)a.gt + ((int64_t)bh * rows + r0 + col) * Lp + M::KPL * g;
-  const E* bp = (const E*)a.qt + ((int64_t)bh * D + col) * Lp + M::KPL * g;
+  const int rt0 = chunk * 8 * kDcRows + w;
+  const E* gt = (const E*)a.gt + (int64_t)bh * rows * Lp;
+  const E* qt = (const E*)a.qt + (int64_t)bh * D * Lp;
 
-  f32x4 acc[D / 16];
+  f32x4 acc[kDcRows][NDT];
 #pragma unroll
-  for (int nd = 0; nd < D / 16; ++nd) acc[nd] = zero4();
-  if (k0 < k1) {
-    F af = ld_frag(ap + k0);
-    F bf[D / 16];
+  for (int i = 0; i < kDcRows; ++i)
 #pragma unroll
-    for (int nd = 0; nd < D / 16; ++nd) bf[nd] = ld_frag(bp + (int64_t)16 * nd * Lp + k0);
-    for (int64_t k = k0; k < k1; k += M::K) {
-      const F ac = af;
-      F bc[D / 16];
+    for (int nd = 0; nd < NDT; ++nd) acc[i][nd] = zero4();
+
+  E qreg[PER][8];
+  F af[kDcRows][KS], an[kDcRows][KS];
+  auto load_q = [&](int64_t kb) {
 #pragma unroll
-      for (int nd = 0; nd < D / 16; ++nd) bc[nd] = bf[nd];
-      if (k + M::K < k1) {
-        af = ld_frag(ap + k + M::K);
+    for (int j = 0; j < PER; ++j) {
+      const int e = tid + 512 * j;
+      if (e < NLD) cp8(qreg[j], qt + (int64_t)(e / (kDcKB / 8)) * Lp + kb + (e % (kDcKB / 8)) * 8);
+    }
+  };
+  auto store_q = [&](int buf) {
 #pragma unroll
-        for (int nd = 0; nd < D / 16; ++nd) bf[nd] = ld_frag(bp + (int64_t)16 * nd * Lp + k + M::K);
+    for (int j = 0; j < PER; ++j) {
+      const int e = tid + 512 * j;
+      if (e < NLD) cp8(qs[buf] + (e / (kDcKB / 8)) * QS + (e % (kDcKB / 8)) * 8, qreg[j]);
+    }
+  };
+  auto load_a = [&](int64_t kb, F (&dst)[kDcRows][KS]) {
+#pragma unroll
+    for (int i = 0; i < kDcRows; ++i) {
+      const int rt = rt0 + 8 * i;
+      if (rt < ntile) {
+        const E* ap = gt + (int64_t)(16 * rt + col) * Lp + kb + M::KPL * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) dst[i][ks] = ld_frag(ap + ks * M::K);
       }
+    }
+  };
+  if (k0 < k1) {
+    load_q(k0);
+    load_a(k0, af);
+  }
+  int buf = 0;
+  for (int64_t kb = k0; kb < k1; kb += kDcKB, buf ^= 1) {
+    store_q(buf);
+    __syncthreads();
+    const bool more = kb + kDcKB < k1;
+    if (more) {
+      load_q(kb + kDcKB);
+      load_a(kb + kDcKB, an);
+    }
 #pragma unroll
-      for (int nd = 0; nd < D / 16; ++nd) acc[nd] = M::mma(ac, bc[nd], acc[nd]);
+    for (int ks = 0; ks < KS; ++ks) {
+      F bq[NDT];
+#pragma unroll
+      for (int nd = 0; nd < NDT; ++nd) bq[nd] = ld_frag(qs[buf] + (16 * nd + col) * QS + ks * M::K + M::KPL * g);
+#pragma unroll
+      for (int i = 0; i < kDcRows; ++i)
+        if (rt0 + 8 * i < ntile)
+#pragma unroll
+          for (int nd = 0; nd < NDT; ++nd) acc[i][nd] = M::mma(af[i][ks], bq[nd], acc[i][nd]);
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < kDcRows; ++i)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) af[i][ks] = an[i][ks];
     }
   }
-  float* out = a.dsum_part + ((int64_t)split * gridDim.y + bh) * rows * D;
+  float* out = a.dsum_part + ((int64_t)split * a.BHn + bh) * rows * D;
 #pragma unroll
-  for (int nd = 0; nd < D / 16; ++nd)
+  for (int i = 0; i < kDcRows; ++i) {
+    const int rt = rt0 + 8 * i;
+    if (rt >= ntile) continue;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[(int64_t)(r0 + 4 * g + r) * D + 16 * nd + col] = acc[nd][r];
+    for (int nd = 0; nd < NDT; ++nd)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[(int64_t)(16 * rt + 4 * g + r) * D + 16 * nd + col] = acc[i][nd][r];
+  }
 }
 
 // dsum = sum over query splits (in split order); rows outside any level are 0.
@@ -683,6 +741,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.dk = dk;
   a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
   a.qsplit = P.qsplit;
+  a.BHn = (int)P.BH;
   a.lp = 0;
   while ((1 << a.lp) < P.S) ++a.lp;
   a.refc = P.p.causal == TA_CAUSAL_REFERENCE;
@@ -706,8 +765,8 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   const unsigned qtiles = (unsigned)(P.Lp / kQueryTile);
   hipLaunchKernelGGL((tree_dq_kernel<E, D>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
   if (P.geo.T > 0) {
-    const unsigned rowtiles = (unsigned)((P.geo.NS + 63) / 64);
-    hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(rowtiles, P.BH, P.qsplit), dim3(256), 0, st, a);
+    const unsigned chunks = (unsigned)((P.geo.NS / 16 + 8 * kDcRows - 1) / (8 * kDcRows));
+    hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(chunks, P.qsplit, P.BH), dim3(512), 0, st, a);
     const int64_t n = P.BH * (int64_t)P.geo.NS * D;
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D);
