@@ -22,6 +22,8 @@
 //   (_treeattn_common.py:70-86).
 // The causal correction adds the same -log A_root to every sample of a
 // query; since sum_s dlogp_s = 0 it has no gradient.
+#include <type_traits>
+
 #include "launch.h"
 
 namespace ta {
@@ -54,7 +56,6 @@ struct TreeArgs {
   int64_t ksb, ksl, ksh;
   int qsplit;
   int BHn;  // B * H
-  int lp;  // log2 of S rounded up to a power of two
   // reference causal mode
   int refc, t0;           // t0: first sampled query row (queries below it are the exact head)
   int64_t nqh;            // B * L * H
@@ -190,26 +191,51 @@ __device__ __forceinline__ void load_slots(const TreeArgs& a, const TileSmem<E>&
   if (tid < kQueryTile) sm.cn[tid] = tid < nq ? a.slot_count[qh0 + (int64_t)tid * a.H] : 0;
 }
 
+// Lane (i - O) of the same 16-lane row (0 past the row start): a DPP row_shr,
+// a register move without an LDS round trip.  row_shl by one likewise.
+template <int O>
+__device__ __forceinline__ int row_shr(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, 0x110 + O, 0xf, 0xf, true);
+}
+template <int O>
+__device__ __forceinline__ float row_shr(float x) {
+  return __builtin_bit_cast(float, row_shr<O>(__builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ int row_shl1(int x) { return __builtin_amdgcn_update_dpp(0, x, 0x101, 0xf, 0xf, true); }
+
+// x from lane u - O of this lane's group of P lanes (the caller masks u < O)
+template <int P, int O, typename T>
+__device__ __forceinline__ T grp_up(T x) {
+  if constexpr (P <= 16) return row_shr<O>(x);
+  else return __shfl_up(x, O, P);
+}
+template <int P>
+__device__ __forceinline__ int grp_down1(int x) {
+  if constexpr (P <= 16) return row_shl1(x);
+  else return __shfl_down(x, 1, P);
+}
+
 // G for depth d, chunk [c0, c0 + ncols) of the level's child rows, into
-// Gm[q][col].  A group of P = 2^lp >= S lanes per query, lane u = slot u
-// (slots ascend by leaf block, so the slots under one child row form a run,
-// and so do the slots under one node).  Segmented inclusive scans over the
-// runs give A_row (sum of dl under the child row) and A_n (under the node).
-// The last lane of each child run writes G[n, j] = A_row - p_j A_n; the last
-// lane of each node run writes -p_j A_n for the node's children without
-// sampled blocks.  Every entry has one writer and every sum a fixed order:
-// deterministic, no atomics.  Clamped logits get 0.
-template <typename E>
-__device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, int S, int lp, int nq,
-                                        float maxhalf, const float* Xs, const int* lf, const float* dls,
-                                        const int* cn, E* Gm, int tid) {
+// Gm[q][col].  A group of P >= S lanes per query, lane u = slot u (slots
+// ascend by leaf block, so the slots under one child row form a run, and so
+// do the slots under one node).  Segmented inclusive scans over the runs give
+// A_row (sum of dl under the child row) and A_n (under the node); for P <= 16
+// the scan steps are DPP row shifts.  The last lane of each child run writes
+// G[n, j] = A_row - p_j A_n; the last lane of each node run writes -p_j A_n
+// for the node's children without sampled blocks.  Every entry has one
+// writer and every sum a fixed order: deterministic, no atomics.  Clamped
+// logits get 0.
+template <typename E, int P>
+__device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols, int S, int nq, float maxhalf,
+                                          const float* Xs, const int* lf, const float* dls, const int* cn, E* Gm,
+                                          int tid) {
+  constexpr int LP = P <= 1 ? 0 : P <= 2 ? 1 : P <= 4 ? 2 : P <= 8 ? 3 : P <= 16 ? 4 : P <= 32 ? 5 : 6;
   const int b = G.b, lb = G.lb;
   const int sh = lb * (G.T - d), sh2 = sh - lb;
-  const int P = 1 << lp;
   const int lane = tid & 63;
-  for (int e0 = 0; e0 < (kQueryTile << lp); e0 += 256) {
+  for (int e0 = 0; e0 < (kQueryTile << LP); e0 += 256) {
     const int e = e0 + tid;
-    const int qi = e >> lp, u = e & (P - 1);
+    const int qi = e >> LP, u = e & (P - 1);
     const int cnt = qi < nq ? cn[qi] : 0;
     const bool act = u < cnt;
     const int leaf = act ? lf[qi * S + u] : 0;
@@ -217,23 +243,40 @@ __device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, 
     const int crow = act ? (leaf >> sh2) : -1 - u;  // inactive lanes: singleton runs
     const int node = act ? (leaf >> sh) : -1 - u;
     float vc = dl, vn = dl;
-    uint64_t has = act ? (1ull << (crow & (b - 1))) : 0ull;  // children of the node with sampled blocks
-    for (int o = 1; o < P; o <<= 1) {
-      const float tc = __shfl_up(vc, o, P);
-      const float tn = __shfl_up(vn, o, P);
-      const int kc = __shfl_up(crow, o, P);
-      const int kn = __shfl_up(node, o, P);
-      const uint64_t th = __shfl_up(has, o, P);
-      if (u >= o) {
-        if (kc == crow) vc += tc;
-        if (kn == node) {
-          vn += tn;
-          has |= th;
+    // children of the node with sampled blocks (b <= 64: two 32-bit words)
+    int has0 = 0, has1 = 0;
+    if (act) {
+      const int j = crow & (b - 1);
+      if (j < 32) has0 = 1 << j;
+      else has1 = 1 << (j - 32);
+    }
+    auto step = [&](auto oc) {
+      constexpr int O = decltype(oc)::value;
+      if constexpr (O < P) {
+        const float tc = grp_up<P, O>(vc);
+        const float tn = grp_up<P, O>(vn);
+        const int kc = grp_up<P, O>(crow);
+        const int kn = grp_up<P, O>(node);
+        const int h0 = grp_up<P, O>(has0);
+        const int h1 = grp_up<P, O>(has1);
+        if (u >= O) {
+          if (kc == crow) vc += tc;
+          if (kn == node) {
+            vn += tn;
+            has0 |= h0;
+            has1 |= h1;
+          }
         }
       }
-    }
-    const int nxc = __shfl_down(crow, 1, P);
-    const int nxn = __shfl_down(node, 1, P);
+    };
+    step(std::integral_constant<int, 1>());
+    step(std::integral_constant<int, 2>());
+    step(std::integral_constant<int, 4>());
+    step(std::integral_constant<int, 8>());
+    step(std::integral_constant<int, 16>());
+    step(std::integral_constant<int, 32>());
+    const int nxc = grp_down1<P>(crow);
+    const int nxn = grp_down1<P>(node);
     const bool last = u + 1 >= cnt;
     const bool cend = act && (last || nxc != crow);
     const bool nend = act && (last || nxn != node);
@@ -257,7 +300,7 @@ __device__ __forceinline__ void build_g(const Geo& G, int d, int c0, int ncols, 
       }
       if (nend) {
         for (int j = 0; j < b; ++j) {
-          if ((has >> j) & 1ull) continue;
+          if (j < 32 ? ((has0 >> j) & 1) : ((has1 >> (j - 32)) & 1)) continue;
           const float x = xr[j];
           const bool live = x >= -maxhalf && x <= maxhalf;
           gr[j] = (E)(live ? -__expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
@@ -306,8 +349,9 @@ __device__ __forceinline__ void sum_rows8_deep(float* acc, const E* rows, int64_
 //   dq^T += C_chunk^T G^T (wave w: head-dim tiles w, w+4, ...)
 // and G^T goes to global for the summary-gradient product.  The epilogue adds
 // the leaf parts dq_pair of each query's distinct blocks.
-template <typename E, int D>
-__global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
+// kP: lanes per query in build_g (16: S <= 16, DPP scans; 64: shuffles).
+template <typename E, int D, int kP>
+__global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   using M = Mfma<E>;
   using F = typename M::frag;
   constexpr int KS = D / M::K;
@@ -438,7 +482,7 @@ __global__ __launch_bounds__(256) void tree_dq_kernel(TreeArgs a) {
       z8(sm.Gm + r * kGS + cc);
     }
     __syncthreads();
-    build_g<E>(G, d, c0, ncols, S, a.lp, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    build_g_p<E, kP>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
     __syncthreads();
     if (a.refc) {
       // boundary-mass gradient of the reference causal mode (ref_causal_grad_kernel)
@@ -742,8 +786,6 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
   a.qsplit = P.qsplit;
   a.BHn = (int)P.BH;
-  a.lp = 0;
-  while ((1 << a.lp) < P.S) ++a.lp;
   a.refc = P.p.causal == TA_CAUSAL_REFERENCE;
   a.t0 = P.L > P.S ? (int)P.S : 0;
   a.nqh = P.B * P.L * P.H;
@@ -760,10 +802,18 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   if (a.refc)
     hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
   const int smem_q = tree_smem(P);
-  hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D>, hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
-  if (e != hipSuccess) return e;
   const unsigned qtiles = (unsigned)(P.Lp / kQueryTile);
-  hipLaunchKernelGGL((tree_dq_kernel<E, D>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
+  if (P.S <= 16) {
+    hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D, 16>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((tree_dq_kernel<E, D, 16>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
+  } else {
+    hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D, 64>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((tree_dq_kernel<E, D, 64>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
+  }
   if (P.geo.T > 0) {
     const unsigned chunks = (unsigned)((P.geo.NS / 16 + 8 * kDcRows - 1) / (8 * kDcRows));
     hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(chunks, P.qsplit, P.BH), dim3(512), 0, st, a);
