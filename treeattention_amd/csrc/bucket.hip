@@ -17,12 +17,14 @@ constexpr int kWin = 2048;                 // leaf blocks per LDS window
 constexpr int kWords = kQueryChunk / 32;  // bitmask words per block
 
 struct BucketArgs {
-  int L, H, S, NL, nchunk;
+  int L, H, S, NL, nchunk, npiece;
   const int* slot_leaf;
   const int* slot_count;
   int* hist;         // (BH, NL, nchunk)
   int* block_start;  // (BH, NL+1)
   int* order;        // (BH, L*S)
+  int* piece_start;  // (BH, NL+1)
+  int* piece_block;  // (BH, npiece)
 };
 
 // grid (nchunk, BH), block kQueryChunk (one thread per query of the chunk).
@@ -70,8 +72,11 @@ __global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) 
   }
 }
 
-// Exclusive scan of hist[bh] (block-major, chunk-minor) in place; one
-// workgroup of 1024 threads per (batch, head).
+// Exclusive scan of hist[bh] (block-major, chunk-minor) in place, the block
+// starts, then the leaf-forward pieces: block beta with n pairs gets
+// ceil(n / kPieceFwd) pieces, numbered by an exclusive scan over beta, and
+// piece_block names each piece's block (-1 past the last).  One workgroup of
+// 1024 threads per (batch, head).
 __global__ __launch_bounds__(1024) void bucket_scan_kernel(BucketArgs a) {
   __shared__ int part[1024];
   const int bh = blockIdx.x, tid = threadIdx.x;
@@ -99,6 +104,32 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(BucketArgs a) {
   int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   for (int beta = tid; beta < a.NL; beta += 1024) bs[beta] = hh[(int64_t)beta * a.nchunk];
   if (tid == 1023) bs[a.NL] = part[1023];
+  __syncthreads();  // block starts (global, this workgroup's writes) visible; part[] reused below
+
+  const int perb = (a.NL + 1023) / 1024;
+  const int b0 = min(a.NL, tid * perb), b1 = min(a.NL, b0 + perb);
+  int np = 0;
+  for (int beta = b0; beta < b1; ++beta) np += (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
+  part[tid] = np;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int v = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int* ps = a.piece_start + (int64_t)bh * (a.NL + 1);
+  int* pb = a.piece_block + (int64_t)bh * a.npiece;
+  int pr = part[tid] - np;
+  for (int beta = b0; beta < b1; ++beta) {
+    ps[beta] = pr;
+    const int m = (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
+    for (int j = 0; j < m; ++j) pb[pr + j] = beta;
+    pr += m;
+  }
+  const int total = part[1023];
+  if (tid == 1023) ps[a.NL] = total;
+  for (int i = total + tid; i < a.npiece; i += 1024) pb[i] = -1;
 }
 
 hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
@@ -113,6 +144,9 @@ hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
   a.hist = (int*)(rec + P.rec.hist);
   a.block_start = (int*)(rec + P.rec.block_start);
   a.order = (int*)(rec + P.rec.order);
+  a.npiece = P.npiece;
+  a.piece_start = (int*)(rec + P.rec.piece_start);
+  a.piece_block = (int*)(rec + P.rec.piece_block);
   hipLaunchKernelGGL(bucket_pass_kernel<false>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
   hipLaunchKernelGGL(bucket_scan_kernel, dim3(P.BH), dim3(1024), 0, st, a);
   hipLaunchKernelGGL(bucket_pass_kernel<true>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);

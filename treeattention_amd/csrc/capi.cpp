@@ -109,6 +109,9 @@ int make_plan(const ta_problem* p, Plan* P) {
   // bucketing: one count per (leaf block, chunk of kQueryChunk queries)
   P->qc = kQueryChunk;
   P->nchunk = (int)((L + kQueryChunk - 1) / kQueryChunk);
+  P->npiece = (int)(NL + (L * S + kPieceFwd - 1) / kPieceFwd);
+  if ((int64_t)P->npiece * P->BH > ((int64_t)1 << 31) - 1)
+    return fail(TA_ERR_UNSUPPORTED, "too many leaf-forward pieces (NL=%lld)", (long long)NL);
   if ((int64_t)NL * P->nchunk * P->BH > ((int64_t)1 << 29))
     return fail(TA_ERR_UNSUPPORTED, "too many leaf blocks x query chunks for the bucket table (NL=%lld)",
                 (long long)NL);
@@ -139,6 +142,8 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.hist = r.take(P->BH * NL * P->nchunk * 4);
   P->rec.block_start = r.take(P->BH * (NL + 1) * 4);
   P->rec.order = r.take(P->BH * L * S * 4);
+  P->rec.piece_start = r.take(P->BH * (NL + 1) * 4);
+  P->rec.piece_block = r.take(P->BH * P->npiece * 4);
   P->rec.dstar = r.take(p->causal == TA_CAUSAL_REFERENCE ? L * 4 : 0);
   P->rec.total = r.at;
   Carver f;

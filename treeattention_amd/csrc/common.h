@@ -288,6 +288,37 @@ __device__ __forceinline__ void sum_rows8(float* acc, const E* rows, int64_t str
   }
 }
 
+// ------------------------------------------------ transposing LDS reads ---
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(8))) short s16x8;
+
+// Four 16-bit values through ds_read_b64_tr_b16, gfx950's transposing LDS
+// read of a row-major tile X (row stride rs elements): within each group of
+// 16 lanes, lane i receives element i%4 of the 8-byte slots that lanes
+// 4r + i/4 (r = 0..3) point at.  Lane j of a group points at row k0 + j/4 and
+// an 8-byte-aligned column c(j%4) of its choice, so lane i gets
+// X[k0 + r][c(i/4) + i%4], r = 0..3.
+template <typename E>
+__device__ __forceinline__ s16x4 tr_read4(const E* X, int rs, int row, int col) {
+  typedef __attribute__((address_space(3))) s16x4* lp;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(X + row * rs + col));
+}
+
+// A-operand fragment of a (head dims x keys) product read from the row-major
+// [key][dim] LDS tile X: tile md = 2p + e, row m <-> dim 32p + 8(m/4) + 4e +
+// m%4 (so that the product's output gives each lane eight consecutive dims),
+// keys in the order of acc_operand for k-step kk (32kk + 4g + i, then
+// 32kk + 16 + 4g + i).
+template <typename E>
+__device__ __forceinline__ typename Mfma<E>::frag perm_dim_frag(const E* X, int rs, int md, int kk, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  const int cc = 32 * (md >> 1) + 8 * (j & 3) + 4 * (md & 1);
+  const s16x4 lo = tr_read4(X, rs, 32 * kk + 4 * g + (j >> 2), cc);
+  const s16x4 hi = tr_read4(X, rs, 32 * kk + 16 + 4 * g + (j >> 2), cc);
+  const s16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Mfma<E>::frag, x);
+}
+
 // ------------------------------------------------------- XCD placement ---
 // Workgroups are dispatched to the 8 XCDs of the chip round-robin by linear
 // id, and each XCD has its own L2.  xcd_bh_block maps linear id i to
@@ -335,6 +366,45 @@ __device__ __forceinline__ float dot_row(const E* q, const float* c, int D) {
 }
 
 // ------------------------------------------------------------ reductions ---
+
+// x op x[lane ^ 16] and x op x[lane ^ 32] through gfx950's v_permlane16_swap
+// and v_permlane32_swap (VALU lane swaps, no LDS round trip).  With both
+// registers holding x, the swap leaves (x[i & ~16], x[i | 16]) (resp. 32) in
+// lane i, whose op is the xor-partner reduction.  The swap is issued as inline
+// asm with both registers as in/out operands: the compiler's own lowering of
+// the two-result builtin has been seen to reuse the first result for both.
+// The s_nops cover the VALU-write -> permlane-read and permlane -> VALU-read
+// distances.
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  return fmaxf(a, b);
+}
+// Sum / max over the four lanes col, col+16, col+32, col+48 (the lane groups
+// of an MFMA accumulator column).
+__device__ __forceinline__ float col_sum(float x) { return xor32_sum(xor16_sum(x)); }
+__device__ __forceinline__ float col_max(float x) { return xor32_max(xor16_max(x)); }
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -393,6 +463,8 @@ struct RecordLayout {
   int64_t hist;        // int (BH, NL, nchunk): pair counts, then scanned offsets
   int64_t block_start; // int (BH, NL + 1)
   int64_t order;       // int (BH, L*S): (l*S + u) grouped by leaf block
+  int64_t piece_start; // int (BH, NL + 1): first leaf-forward piece of each block, exclusive scan
+  int64_t piece_block; // int (BH, npiece): leaf block of each piece, -1 past the last
   int64_t dstar;       // int (L): reference causal mode: first uncorrected depth per query
   int64_t total;
 };
@@ -417,5 +489,10 @@ struct BwdWorkspaceLayout {
 };
 
 constexpr int kQueryChunk = 256; // queries per bucketing chunk (one wavefront each)
+// A leaf block's pairs are cut into pieces of at most kPieceFwd pairs, one
+// leaf-forward workgroup each, so the heavy low blocks of causal runs (a
+// block near the start is reachable from every later query) do not leave
+// one workgroup running long after the others.
+constexpr int kPieceFwd = 512;
 
 }  // namespace ta

@@ -13,6 +13,7 @@ struct Plan {
   int esize;        // bytes per element of q/k/v
   int qc;           // queries per bucketing chunk
   int nchunk;       // bucketing chunks per (batch, head)
+  int npiece;       // leaf-forward pieces per (batch, head), upper bound
   int64_t Lp;       // L rounded up to a multiple of kQueryTile
   int qsplit;       // query splits of the summary-gradient product
   RecordLayout rec;

@@ -259,24 +259,13 @@ struct BwdTrTile {
   static constexpr int bytes = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
 };
 
-typedef __attribute__((ext_vector_type(4))) short s16x4;
-
-// Four 16-bit values [k0..k0+3][n] of a row-major LDS tile X (row stride rs
-// elements) for lane i = n - n0 of each 16-lane group; `row` = k0 + (lane%16)/4,
-// `col` = n0 + 4 (lane % 4).
-template <typename E>
-__device__ __forceinline__ s16x4 tr_read(const E* X, int rs, int row, int col) {
-  typedef __attribute__((address_space(3))) s16x4* lp;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(X + row * rs + col));
-}
 
 // An MFMA operand fragment of k = 8 values: rows k0a..k0a+3 then k0b..k0b+3.
 template <typename E>
 __device__ __forceinline__ typename Mfma<E>::frag tr_frag(const E* X, int rs, int k0a, int k0b, int n0, int lane) {
   const int j = lane & 15;
-  const s16x4 lo = tr_read(X, rs, k0a + (j >> 2), n0 + 4 * (j & 3));
-  const s16x4 hi = tr_read(X, rs, k0b + (j >> 2), n0 + 4 * (j & 3));
-  typedef __attribute__((ext_vector_type(8))) short s16x8;
+  const s16x4 lo = tr_read4(X, rs, k0a + (j >> 2), n0 + 4 * (j & 3));
+  const s16x4 hi = tr_read4(X, rs, k0b + (j >> 2), n0 + 4 * (j & 3));
   const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(typename Mfma<E>::frag, v);
 }
@@ -367,30 +356,35 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
         pacc[mt] = M::mma(ld_frag(vp + ks * M::K), gc.f[ks], pacc[mt]);
       }
     }
+    // keys < kmax are visible; masking only when some pair of the tile needs it
     const int kmax = valid ? (a.causal ? min(LB, l + (a.N - a.L) - beta * LB + 1) : LB) : 0;
+    if (__any(kmax < LBP)) {
+#pragma unroll
+      for (int mt = 0; mt < LBP / 16; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sacc[mt][r] = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < LBP / 16; ++mt) sacc[mt] *= a.scale_log2;
+    }
     float mx = -__builtin_inff();
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float sv = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
-        sacc[mt][r] = sv;
-        mx = fmaxf(mx, sv);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, fmaxf(fmaxf(sacc[mt][0], sacc[mt][1]), fmaxf(sacc[mt][2], sacc[mt][3])));
+    mx = col_max(mx);
+    if (mx == -__builtin_inff()) mx = 0.f;  // no visible key (padding pairs): all p = 0
     float sum = 0.f;
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = (16 * mt + 4 * g + r) < kmax ? exp2f(sacc[mt][r] - mx) : 0.f;
+        const float pv = __builtin_amdgcn_exp2f(sacc[mt][r] - mx);
         sacc[mt][r] = pv;
         sum += pv;
       }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    sum = col_sum(sum);
+    const float inv = sum > 0.f ? __builtin_amdgcn_rcpf(sum) : 0.f;
     float delta = 0.f;
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt)
@@ -399,8 +393,7 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
         sacc[mt][r] *= inv;
         delta += sacc[mt][r] * pacc[mt][r];
       }
-    delta += __shfl_xor(delta, 16, 64);
-    delta += __shfl_xor(delta, 32, 64);
+    delta = col_sum(delta);
     const float wt = valid ? a.slot_weight[qh * S + u] : 0.f;
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt)
@@ -410,14 +403,28 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
 
     // dq_pair^T = K^T dz^T: K^T fragments read transposed from Ks in the
     // accumulator's key order (keys 32ks + 4g.. and 32ks + 16 + 4g..)
-    E* dqp = (E*)a.dq_part + (qh * S + u) * D;
+    // K^T fragments with permuted head dims: each lane ends with eight
+    // consecutive dims of its pair's dq row, one 16-byte store per 32 dims
+    E* dqp = (E*)a.dq_part + (qh * S + u) * D + 8 * g;
 #pragma unroll
-    for (int md = 0; md < D / 16; ++md) {
-      f32x4 o = zero4();
+    for (int p = 0; p < D / 32; ++p) {
+      f32x4 o0 = zero4(), o1 = zero4();
 #pragma unroll
-      for (int ks = 0; ks < LBP / M::K; ++ks)
-        o = M::mma(tr_frag(Ks, RS, 32 * ks + 4 * g, 32 * ks + 16 + 4 * g, 16 * md, lane), acc_operand<E>(pacc, ks), o);
-      if (valid) store4(dqp + 16 * md + 4 * g, o, a.scale);
+      for (int ks = 0; ks < LBP / M::K; ++ks) {
+        const typename M::frag z = acc_operand<E>(pacc, ks);
+        o0 = M::mma(perm_dim_frag<E>(Ks, RS, 2 * p, ks, lane), z, o0);
+        o1 = M::mma(perm_dim_frag<E>(Ks, RS, 2 * p + 1, ks, lane), z, o1);
+      }
+      if (valid) {
+        typedef __attribute__((ext_vector_type(8))) E e8;
+        e8 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          o[r] = (E)(o0[r] * a.scale);
+          o[4 + r] = (E)(o1[r] * a.scale);
+        }
+        *(e8*)(dqp + 32 * p) = o;
+      }
     }
 
     __syncthreads();  // phase B of the previous tile is done with the staging tiles

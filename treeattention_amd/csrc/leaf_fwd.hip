@@ -15,12 +15,14 @@
 namespace ta {
 
 struct LeafFwdArgs {
-  int B, L, H, S, NL, LB, causal, coff;
+  int B, L, H, S, NL, LB, causal, coff, npiece;
   float scale_log2;
   const void *q, *k, *v;
   int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh;
   const int* order;
   const int* block_start;
+  const int* piece_start;
+  const int* piece_block;
   const float* slot_weight;
   void* partial;
 };
@@ -138,6 +140,170 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
   }
 }
 
+// 16-bit inputs.  One workgroup (four waves) per piece of at most kPieceFwd
+// pairs of one leaf block (bucket.hip), so the heavy low blocks of causal runs
+// are spread over many workgroups.  Every wave keeps the block's K rows (the
+// A operand of S^T = K Q^T) and V^T (the A operand of O^T = V^T P^T) in
+// registers for the whole piece; V^T is read from a row-major LDS copy with
+// transposing reads whose head-dim order puts eight consecutive dims of a
+// pair's output in one lane, so each output row leaves in 16-byte stores.
+// The piece's pair list sits in LDS and every wave loads the query rows of
+// its next two 16-pair tiles while the current one computes.
+template <typename E, int D, int LBP>
+__global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
+  using M = Mfma<E>;
+  using F = typename M::frag;
+  constexpr int KS = D / M::K;      // k-steps of S^T over head dims
+  constexpr int MT = LBP / 16;      // key tiles of S^T
+  constexpr int KK = LBP / M::K;    // k-steps of O^T over keys
+  constexpr int NP = D / 32;        // 32-dim output groups (two O^T tiles each)
+  constexpr bool kKreg = LBP * D <= 64 * 128;
+  constexpr int VS = D + 16;        // padded LDS row stride (elements)
+  extern __shared__ __align__(16) char smem[];
+  int* ord_s = (int*)smem;                  // [kPieceFwd] (l << 6) | u
+  E* Vs = (E*)(smem + kPieceFwd * 4);       // [LBP][VS]
+  E* Ks = Vs + LBP * VS;                    // [LBP][VS] (K in LDS when it does not fit in registers)
+
+  int bh, piece;
+  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.npiece, bh, piece)) return;
+  const int beta = a.piece_block[(int64_t)bh * a.npiece + piece];
+  if (beta < 0) return;
+  const int bb = bh / a.H, h = bh - bb * a.H;
+  const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
+  const int p0 = bs[beta] + (piece - a.piece_start[(int64_t)bh * (a.NL + 1) + beta]) * kPieceFwd;
+  const int np = min(bs[beta + 1] - p0, kPieceFwd);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int LB = a.LB, S = a.S;
+  const E* q = (const E*)a.q;
+  const E* k = (const E*)a.k;
+  const E* v = (const E*)a.v;
+
+  const int* ord = a.order + (int64_t)bh * a.L * S + p0;
+  for (int i = tid; i < np; i += 256) {
+    const int ent = ord[i];
+    const int l = ent / S;
+    ord_s[i] = (l << 6) | (ent - l * S);
+  }
+  for (int e = tid; e < LBP * D / 8; e += 256) {
+    const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+    uint4 vv = make_uint4(0, 0, 0, 0), kv = make_uint4(0, 0, 0, 0);
+    if (key < LB) {
+      const int64_t tok = (int64_t)beta * LB + key;
+      vv = *(const uint4*)(v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+      if (!kKreg && k) kv = *(const uint4*)(k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+    }
+    *(uint4*)(Vs + key * VS + c) = vv;
+    if constexpr (!kKreg) *(uint4*)(Ks + key * VS + c) = kv;
+  }
+  // K rows straight from global memory into A fragments (zero past LB)
+  F kf[kKreg ? MT : 1][KS];
+  if constexpr (kKreg) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int key = 16 * mt + col;
+      const E* kr = (k && key < LB) ? k + bb * a.ksb + ((int64_t)beta * LB + key) * a.ksl + h * a.ksh : nullptr;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = kr ? ld_frag(kr + ks * M::K + M::KPL * g) : zero_frag<E>();
+    }
+  }
+  __syncthreads();
+  // V^T fragments (dims x keys), dims permuted so each lane's outputs are
+  // eight consecutive dims
+  F vf[2 * NP][KK];
+#pragma unroll
+  for (int md = 0; md < 2 * NP; ++md)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) vf[md][kk] = perm_dim_frag<E>(Vs, VS, md, kk, lane);
+
+  const int ntile = (np + 15) >> 4;
+  const int coff = a.coff - beta * LB;  // key j of the block is visible to query l iff j <= l + coff
+  auto qrow = [&](int t) -> const E* {
+    const int i = 16 * t + col;
+    if (t >= ntile || i >= np) return nullptr;
+    return q + bb * a.qsb + (int64_t)(ord_s[i] >> 6) * a.qsl + h * a.qsh;
+  };
+  RowFrags<E, D> qb[3];
+  qb[0].load(qrow(w), g);
+  qb[1].load(qrow(w + 4), g);
+  auto step = [&](int t, RowFrags<E, D>& cur, RowFrags<E, D>& nxt) {
+    const int i = 16 * t + col;
+    const bool valid = i < np;
+    const int ent = valid ? ord_s[i] : 0;
+    const int l = ent >> 6, u = ent & 63;
+    nxt.load(qrow(t + 8), g);
+    f32x4 sacc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      sacc[mt] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if constexpr (kKreg) sacc[mt] = M::mma(kf[mt][ks], cur.f[ks], sacc[mt]);
+        else sacc[mt] = M::mma(ld_frag(Ks + (16 * mt + col) * VS + ks * M::K + M::KPL * g), cur.f[ks], sacc[mt]);
+      }
+    }
+    const int kmax = valid ? (a.causal ? min(LB, l + coff + 1) : LB) : 0;
+    float mx = -__builtin_inff();
+    if (__any(kmax < LBP)) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sacc[mt][r] = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) sacc[mt] *= a.scale_log2;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) mx = fmaxf(mx, fmaxf(fmaxf(sacc[mt][0], sacc[mt][1]), fmaxf(sacc[mt][2], sacc[mt][3])));
+    mx = col_max(mx);
+    if (mx == -__builtin_inff()) mx = 0.f;  // no visible key (padding lanes): all p = 0
+    float sum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = __builtin_amdgcn_exp2f(sacc[mt][r] - mx);
+        sacc[mt][r] = p;
+        sum += p;
+      }
+    sum = col_sum(sum);
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+    const float f = (valid && sum > 0.f) ? a.slot_weight[qh * S + u] * __builtin_amdgcn_rcpf(sum) : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sacc[mt] *= f;
+    F pf[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) pf[kk] = acc_operand<E>(sacc, kk);
+    E* dst = (E*)a.partial + (qh * S + u) * D + 8 * g;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      f32x4 o0 = zero4(), o1 = zero4();
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        o0 = M::mma(vf[2 * p][kk], pf[kk], o0);
+        o1 = M::mma(vf[2 * p + 1][kk], pf[kk], o1);
+      }
+      if (valid) {
+        typedef __attribute__((ext_vector_type(8))) E e8;
+        e8 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          o[r] = (E)o0[r];
+          o[4 + r] = (E)o1[r];
+        }
+        *(e8*)(dst + 32 * p) = o;
+      }
+    }
+  };
+  for (int t = w; t < ntile; t += 12) {
+    step(t, qb[0], qb[2]);
+    if (t + 4 >= ntile) break;
+    step(t + 4, qb[1], qb[0]);
+    if (t + 8 >= ntile) break;
+    step(t + 8, qb[2], qb[1]);
+  }
+}
+
 // out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
@@ -165,8 +331,13 @@ static int fwd_smem_t() {
   return fwd_smem(D, LBP, (int)sizeof(E));
 }
 
+static int fwd16_smem(int D, int LBP) {
+  return kPieceFwd * 4 + (LBP * D <= 64 * 128 ? 1 : 2) * LBP * (D + 16) * 2;
+}
+
 int leaf_fwd_smem(const Plan& P) {
-  const int s = fwd_smem((int)P.D, padded_keys(P.geo.LB), P.esize);
+  const int s = P.esize == 2 ? fwd16_smem((int)P.D, padded_keys(P.geo.LB))
+                             : fwd_smem((int)P.D, padded_keys(P.geo.LB), P.esize);
   return s <= 160 * 1024 ? s : -1;
 }
 
@@ -191,13 +362,24 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   a.vsb = P.p.v_strides[0]; a.vsl = P.p.v_strides[1]; a.vsh = P.p.v_strides[2];
   a.order = (const int*)(rec + P.rec.order);
   a.block_start = (const int*)(rec + P.rec.block_start);
+  a.npiece = P.npiece;
+  a.piece_start = (const int*)(rec + P.rec.piece_start);
+  a.piece_block = (const int*)(rec + P.rec.piece_block);
   a.slot_weight = (const float*)(rec + P.rec.slot_weight);
   a.partial = ws + P.fws.partial;
-  const int smem = fwd_smem_t<E, D, LBP>();
-  hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.geo.NL)), dim3(256), smem, st, a);
+  if constexpr (sizeof(E) == 2) {
+    const int smem = fwd16_smem(D, LBP);
+    hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd16_kernel<E, D, LBP>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((leaf_fwd16_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.npiece)), dim3(256), smem, st, a);
+  } else {
+    const int smem = fwd_smem_t<E, D, LBP>();
+    hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.geo.NL)), dim3(256), smem, st, a);
+  }
   const int64_t nqh = P.B * P.L * P.H;
   const int64_t nthr = nqh * (D / 8);
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
