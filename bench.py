@@ -265,6 +265,13 @@ def main() -> int:
         except Exception as ex:  # no fused backend for this shape
             sdpa = {"skipped": str(ex)[:200]}
 
+    # practical HBM ceiling of this GPU: a plain 1 GiB device copy (1 GiB read + 1 GiB written)
+    src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    copy_ms = min(timed(lambda: dst.copy_(src), 1) for _ in range(5))
+    copy_gbs = 2 * src.numel() * src.element_size() / (copy_ms / 1e3) / 1e9
+    del src, dst
+
     cpu = None if args.no_cpu else cpu_baseline(cfg)
     step_ms = res["step_ms"]
     line = {
@@ -289,6 +296,7 @@ def main() -> int:
         "phase_ms": {k_: round(v_, 4) for k_, v_ in phase_ms.items()},
         "phase_roofline": per_phase,
         "roofline": roofline,
+        "hbm_copy_GBs": round(copy_gbs, 1),
         "cpu_baseline": cpu,
         "gpu_vs_cpu": round((B * L / (step_ms / 1e3)) / cpu["value"], 1) if cpu else None,
         "sdpa_baseline": sdpa,

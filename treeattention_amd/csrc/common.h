@@ -256,35 +256,40 @@ __device__ __forceinline__ void mfma_rows(const RowFrags<E, D>& A, float* X, int
 }
 
 // acc[0..8) += sum_{u < n} rows[u*stride .. +8) (E values, 16-byte aligned
-// when E is 16-bit), in u order; four rows' loads are in flight at once.
+// when E is 16-bit), in u order.  16-bit rows are loaded sixteen at a time as
+// raw 16-byte words (converted after the loads), float rows eight at a time,
+// so that many loads are in flight per thread.
 template <typename E>
 __device__ __forceinline__ void sum_rows8(float* acc, const E* rows, int64_t stride, int n) {
-  int u = 0;
-  for (; u + 4 <= n; u += 4) {
-    float x[4][8];
+  if constexpr (sizeof(E) == 2) {
+    for (int u0 = 0; u0 < n; u0 += 16) {
+      uint4 x[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const E* p = rows + (int64_t)(u + j) * stride;
-      if constexpr (sizeof(E) == 2) {
+      for (int j = 0; j < 16; ++j)
+        x[j] = u0 + j < n ? *(const uint4*)(rows + (int64_t)(u0 + j) * stride) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
         typedef __attribute__((ext_vector_type(8))) E v8;
-        const v8 v = *(const v8*)p;
+        const v8 v = __builtin_bit_cast(v8, x[j]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[j][i] = (float)v[i];
-      } else {
-        const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-        x[j][0] = a.x; x[j][1] = a.y; x[j][2] = a.z; x[j][3] = a.w;
-        x[j][4] = b.x; x[j][5] = b.y; x[j][6] = b.z; x[j][7] = b.w;
+        for (int i = 0; i < 8; ++i) acc[i] += (float)v[i];
       }
     }
+  } else {
+    for (int u0 = 0; u0 < n; u0 += 8) {
+      float4 x[8][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 8; ++j) {
+        const float* p = (const float*)rows + (int64_t)(u0 + j) * stride;
+        x[j][0] = u0 + j < n ? *(const float4*)p : make_float4(0, 0, 0, 0);
+        x[j][1] = u0 + j < n ? *(const float4*)(p + 4) : make_float4(0, 0, 0, 0);
+      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += x[j][i];
-  }
-  for (; u < n; ++u) {
-    const E* p = rows + (int64_t)u * stride;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += (float)p[i];
+      for (int j = 0; j < 8; ++j) {
+        acc[0] += x[j][0].x; acc[1] += x[j][0].y; acc[2] += x[j][0].z; acc[3] += x[j][0].w;
+        acc[4] += x[j][1].x; acc[5] += x[j][1].y; acc[6] += x[j][1].z; acc[7] += x[j][1].w;
+      }
+    }
   }
 }
 

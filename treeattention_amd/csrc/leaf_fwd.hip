@@ -318,8 +318,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ part
   sum_rows8(acc, partial + qh * S * D + 8 * part, D, slot_count[qh]);
   const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
   E* o = out + bb * osb + l * osl + h * osh + 8 * part;
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(8))) E e8;
+    e8 v;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = (E)acc[i];
+    for (int i = 0; i < 8; ++i) v[i] = (E)acc[i];
+    *(e8*)o = v;
+  } else {
+    *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *(float4*)(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
 }
 
 static int fwd_smem(int D, int LBP, int es) {

@@ -27,8 +27,8 @@ __device__ __forceinline__ void load8f(const f16* p, float* o) {
 }
 
 // Leaf-block means of the keys: one workgroup per (leaf block, batch), each
-// thread owns 8 contiguous (head, dim) elements and streams the block's rows.
-// grid (NL, B); means (B*H, NL, D) float.
+// thread owns 8 contiguous (head, dim) elements and streams the block's rows
+// with eight 16-byte loads in flight.  grid (NL, B); means (B*H, NL, D) float.
 template <typename E>
 __global__ __launch_bounds__(256) void block_means_kernel(const E* __restrict__ k, float* __restrict__ means,
                                                           int H, int D, int NL, int LB,
@@ -40,16 +40,25 @@ __global__ __launch_bounds__(256) void block_means_kernel(const E* __restrict__ 
     const int h = (e * 8) / D, d0 = e * 8 - h * D;
     const E* p = k + bb * sb + (int64_t)beta * LB * sl + h * sh + d0;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 4
-    for (int t = 0; t < LB; ++t) {
+    int t = 0;
+    for (; t + 8 <= LB; t += 8) {
+      float x[8][8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) load8f(p + (int64_t)(t + j) * sl, x[j]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += x[j][i];
+    }
+    for (; t < LB; ++t) {
       float x[8];
       load8f(p + (int64_t)t * sl, x);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] += x[i];
     }
     float* o = means + (((int64_t)bb * H + h) * NL + beta) * D + d0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = acc[i] * inv;
+    *(float4*)o = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+    *(float4*)(o + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
   }
 }
 
@@ -65,60 +74,110 @@ struct SumArgs {
   void* sum_t;          // E or float (BH, D, NS+pad)
 };
 
-// One thread per (summary row, dim).  grid (ceil((NS+pad)*D/256), BH).
+// One workgroup per tile of 32 summary rows of one (batch, head); each
+// thread computes 8 dims of one row (vector loads of the block means), writes
+// the float, hi and lo rows with 16-byte stores and stages hi in LDS so the
+// transposed copy (D, NS) leaves as 32-row (64-byte) pieces per head dim.
+// Levels are padded to multiples of 32 rows, so a tile never spans two
+// levels.  grid (NS / 32, BH), block 256.
+constexpr int kSumRows = 32;
+
 template <typename E>
 __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
   const Geo& G = a.geo;
   const int bh = blockIdx.y;
   const int rows = G.NS;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)rows * a.D) return;
-  const int r = (int)(e / a.D), d = (int)(e - (int64_t)r * a.D);
-  float val = 0.f;
+  const int r0 = blockIdx.x * kSumRows;
+  const int D = a.D, nv = D / 8;
+  __shared__ __align__(16) float tile[kSumRows * (128 + 4)];  // [row][D + 4], hi values as float
   int lam = 1;
-  while (lam < G.T && r >= G.off[lam + 1]) ++lam;
-  const int i = r - G.off[lam];
-  if (i < G.pw[lam]) {  // rows past a level's b^lam nodes pad it to a multiple of 32
-    if (a.mode == TA_TREE_NATURAL) {
-      const int per = G.NL / G.pw[lam];
-      const float* m = a.means + ((int64_t)bh * G.NL + (int64_t)i * per) * a.D + d;
-      float s = 0.f;
-      for (int t = 0; t < per; ++t) s += m[(int64_t)t * a.D];
-      val = 0.5f * s / (float)per;
-    } else {
-      // binary: row = off[d+1] + 2*i' + j for heap node n = 2^d - 1 + i'
-      const int depth = lam - 1;
-      const int ip = i >> 1, j = i & 1;
-      const int n = (1 << depth) - 1 + ip;
-      float coef;
-      if (a.mode == TA_TREE_COMPAT) {
-        const int p = n + 1;
-        const int w = p & (-p);
-        const float* m = a.means + (int64_t)bh * G.NL * a.D + d;
-        float sl = 0.f, sr = 0.f;
-        for (int t = 0; t < w; ++t) {
-          sl += m[(int64_t)(p - w + t) * a.D];
-          sr += m[(int64_t)(p + t) * a.D];
+  while (lam < G.T && r0 >= G.off[lam + 1]) ++lam;
+  for (int e = threadIdx.x; e < kSumRows * nv; e += blockDim.x) {
+    const int rr = e / nv, d0 = (e - rr * nv) * 8;
+    const int r = r0 + rr;
+    const int i = r - G.off[lam];
+    float val[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (i < G.pw[lam]) {  // rows past a level's b^lam nodes pad it to a multiple of 32
+      if (a.mode == TA_TREE_NATURAL) {
+        const int per = G.NL / G.pw[lam];
+        const float* m = a.means + ((int64_t)bh * G.NL + (int64_t)i * per) * D + d0;
+        for (int t = 0; t < per; ++t) {
+          float x[8];
+          load8f(m + (int64_t)t * D, x);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) val[j] += x[j];
         }
-        coef = 0.5f * (sl - sr) / (float)w;
+        const float f = 0.5f / (float)per;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) val[j] *= f;
       } else {
-        const int bb = bh / a.H, h = bh - bb * a.H;
-        const E* kn = (const E*)a.knodes;
-        coef = tof(kn[bb * a.ksb + (int64_t)n * a.ksl + h * a.ksh + d]);
+        // binary: row = off[d+1] + 2*i' + j for heap node n = 2^d - 1 + i'
+        const int depth = lam - 1;
+        const int ip = i >> 1, jj = i & 1;
+        const int n = (1 << depth) - 1 + ip;
+        float coef[8];
+        if (a.mode == TA_TREE_COMPAT) {
+          const int p = n + 1;
+          const int w = p & (-p);
+          const float* m = a.means + (int64_t)bh * G.NL * D + d0;
+          float sl[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          for (int t = 0; t < w; ++t) {
+            float xl[8], xr[8];
+            load8f(m + (int64_t)(p - w + t) * D, xl);
+            load8f(m + (int64_t)(p + t) * D, xr);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { sl[j] += xl[j]; sr[j] += xr[j]; }
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) coef[j] = 0.5f * (sl[j] - sr[j]) / (float)w;
+        } else {
+          const int bb = bh / a.H, h = bh - bb * a.H;
+          const E* kn = (const E*)a.knodes + bb * a.ksb + (int64_t)n * a.ksl + h * a.ksh + d0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) coef[j] = tof(kn[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) val[j] = jj == 0 ? 0.5f * coef[j] : -0.5f * coef[j];
       }
-      val = j == 0 ? 0.5f * coef : -0.5f * coef;
+    }
+    const int64_t row_off = ((int64_t)bh * rows + r) * D + d0;
+    *(float4*)(a.sum32 + row_off) = make_float4(val[0], val[1], val[2], val[3]);
+    *(float4*)(a.sum32 + row_off + 4) = make_float4(val[4], val[5], val[6], val[7]);
+    float* tr = tile + rr * (128 + 4) + d0;
+    if constexpr (sizeof(E) == 2) {
+      typedef __attribute__((ext_vector_type(8))) E e8;
+      e8 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        hi[j] = (E)val[j];
+        lo[j] = (E)(val[j] - (float)hi[j]);
+        tr[j] = (float)hi[j];
+      }
+      *(e8*)((E*)a.sum_hi + row_off) = hi;
+      *(e8*)((E*)a.sum_lo + row_off) = lo;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tr[j] = val[j];
     }
   }
-  const int64_t row_off = ((int64_t)bh * rows + r) * a.D + d;
-  a.sum32[row_off] = val;
-  const int64_t t_off = ((int64_t)bh * a.D + d) * rows + r;
-  if constexpr (sizeof(E) == 2) {
-    const E hi = (E)val;
-    ((E*)a.sum_hi)[row_off] = hi;
-    ((E*)a.sum_lo)[row_off] = (E)(val - (float)hi);
-    ((E*)a.sum_t)[t_off] = hi;
-  } else {
-    ((float*)a.sum_t)[t_off] = val;
+  __syncthreads();
+  // transposed copy: (bh, d, r0 .. r0 + 31), eight rows per store
+  for (int e = threadIdx.x; e < D * (kSumRows / 8); e += blockDim.x) {
+    const int d = e / (kSumRows / 8), q0 = (e - d * (kSumRows / 8)) * 8;
+    const int64_t t_off = ((int64_t)bh * D + d) * rows + r0 + q0;
+    if constexpr (sizeof(E) == 2) {
+      typedef __attribute__((ext_vector_type(8))) E e8;
+      e8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (E)tile[(q0 + j) * (128 + 4) + d];
+      *(e8*)((E*)a.sum_t + t_off) = o;
+    } else {
+      float* o = (float*)a.sum_t + t_off;
+      *(float4*)o = make_float4(tile[q0 * 132 + d], tile[(q0 + 1) * 132 + d], tile[(q0 + 2) * 132 + d],
+                                tile[(q0 + 3) * 132 + d]);
+      *(float4*)(o + 4) = make_float4(tile[(q0 + 4) * 132 + d], tile[(q0 + 5) * 132 + d],
+                                      tile[(q0 + 6) * 132 + d], tile[(q0 + 7) * 132 + d]);
+    }
   }
 }
 
@@ -154,8 +213,8 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   a.sum_hi = rec + P.rec.sum_hi;
   a.sum_lo = rec + P.rec.sum_lo;
   a.sum_t = rec + P.rec.sum_t;
-  const int64_t n = (int64_t)G.NS * P.D;
-  hipLaunchKernelGGL(summaries_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
+  if (G.NS > 0)
+    hipLaunchKernelGGL(summaries_kernel<E>, dim3((unsigned)(G.NS / kSumRows), P.BH), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

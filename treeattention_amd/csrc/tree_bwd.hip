@@ -310,38 +310,6 @@ __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols
   }
 }
 
-// acc[0..8) += sum_{u < n} rows[u*stride .. +8), in u order, with up to eight
-// rows' loads in flight.
-template <typename E>
-__device__ __forceinline__ void sum_rows8_deep(float* acc, const E* rows, int64_t stride, int n) {
-  for (int u0 = 0; u0 < n; u0 += 8) {
-    float x[8][8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (u0 + j < n) {
-        const E* p = rows + (int64_t)(u0 + j) * stride;
-        if constexpr (sizeof(E) == 2) {
-          typedef __attribute__((ext_vector_type(8))) E v8;
-          const v8 v = *(const v8*)p;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) x[j][i] = (float)v[i];
-        } else {
-          const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-          x[j][0] = a.x; x[j][1] = a.y; x[j][2] = a.z; x[j][3] = a.w;
-          x[j][4] = b.x; x[j][5] = b.y; x[j][6] = b.z; x[j][7] = b.w;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[j][i] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += x[j][i];
-  }
-}
-
 // One workgroup per 64 queries of one (batch, head).  All 64 query rows are
 // held by every wave as MFMA fragments.  Per chunk of a level's child rows:
 //   X^T = C_chunk Q^T   (wave w: column tiles w, w+4, ...; C rows from global)
@@ -558,10 +526,18 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = stage[qi * SS + d0 + i];
-    sum_rows8_deep(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
+    sum_rows8(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
     E* o = dq + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + d0;
+    if constexpr (sizeof(E) == 2) {
+      typedef __attribute__((ext_vector_type(8))) E e8;
+      e8 v;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (E)acc[i];
+      for (int i = 0; i < 8; ++i) v[i] = (E)acc[i];
+      *(e8*)o = v;
+    } else {
+      *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *(float4*)(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
   }
 }
 
