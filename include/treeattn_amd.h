@@ -1,5 +1,6 @@
 /*
- * treeattn_amd.h -- C ABI of the MI355X (gfx950) stochastic tree-attention library.
+ * treeattn_amd.h -- C ABI of the MI355X (gfx950) tree-attention library (stochastic and
+ * deterministic modes).
  *
  * Plain C: pointers, sizes and a HIP stream.  No torch types cross this
  * boundary.  The caller allocates every buffer (outputs, the saved record and
@@ -171,6 +172,44 @@ int ta_tree_backward(const ta_problem* p, const void* q, const float* weights, c
 int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v,
                 const void* grad_out, const float* weights, const void* record,
                 void* dq, void* dk, void* dv, void* workspace, void* stream);
+
+/* ---- deterministic (exact) mode, reference tree: binary, one token per leaf,
+ * N = 2^T leaves, heap-ordered node keys (_tree_mha.py:271-321).  Rows are
+ * (batch, head, query) rows laid out one after another; the dense products
+ * around these calls (node logits X = Q K^T, out = W V and their gradients)
+ * are plain batched GEMMs the caller runs.  N <= TA_DET_MAX_LEAVES. */
+#define TA_DET_MAX_LEAVES 32768
+
+/* W[r, n] = leaf-n weight of row r from its node logits X[r, 0..N-1)
+ * (row strides ldx, ldw floats): prod of sigmoid(+-x) along n's path, or with
+ * `causal` the softmax of the path log-probabilities over leaves n <= l, where
+ * l = r % L is the row's query position.  Replaces the level loop and the
+ * mask / softmax / exp of _deterministic_attention (_tree_mha.py:286-315). */
+int ta_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw, int64_t rows, int64_t L,
+                   int64_t N, int causal, void* stream);
+
+/* Node-logit gradient of every row, written over X: with dW = dout . v^T per
+ * leaf, dlogw = W (dW - delta) (delta = sum_n W dW if causal, else 0) and
+ * G[node] = sigmoid(-x) A_left - sigmoid(x) A_right, A = dlogw summed over a
+ * child's leaves.  Replaces the autograd of _deterministic_attention
+ * (_tree_mha.py:271-321) up to the GEMMs dq = G K, dK = G^T Q, dv = W^T dout. */
+int ta_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows,
+                int64_t N, int causal, void* stream);
+
+/* Heap-ordered Haar node keys of k (B, N, H, D with element strides
+ * k_strides = {batch, position, head}) into out (N-1, B, H, D) float:
+ * node m, p = m + 1, w = lowest set bit of p:
+ * key = (mean k[p-w, p) - mean k[p, p+w)) / 2.  Replaces
+ * haar_internal_node_keys (_treeattn_common.py:54-86) as read in heap order
+ * by the op (_tree_mha.py:288-291). */
+int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, int64_t B, int64_t H,
+                 int64_t D, int64_t N, void* stream);
+
+/* dk (B, N, H, D, strides dk_strides, fully overwritten) = transpose of
+ * ta_haar_keys applied to dkey (N-1, B, H, D) float.  Replaces the autograd of
+ * haar_internal_node_keys (_treeattn_common.py:70-86). */
+int ta_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* dk_strides, int64_t B,
+                         int64_t H, int64_t D, int64_t N, void* stream);
 
 #ifdef __cplusplus
 }

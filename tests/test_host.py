@@ -105,21 +105,46 @@ def test_adapter_metadata():
     assert not ad.is_compatible(torch.bfloat16, 80, False)[0]
 
 
-def test_attn_fn_requires_num_samples(monkeypatch):
+def test_attn_fn_deterministic_mode_checks(monkeypatch):
+    # TREEATTN_NUM_SAMPLES unset -> the reference adapter's deterministic mode
+    # (baselines/treeattn_torch.py:55-56): power-of-two seqlen, reference tree,
+    # device tensors
     monkeypatch.delenv("TREEATTN_NUM_SAMPLES", raising=False)
     x = torch.zeros(1, 16, 1, 32)
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="device"):
+        ta.attn_fn(x, x, x, False, None)
+    y = torch.zeros(1, 12, 1, 32)
+    with pytest.raises(ValueError, match="power-of-two"):
+        ta.attn_fn(y, y, y, False, None)
+    monkeypatch.setenv("TREEATTN_BRANCHING", "4")
+    with pytest.raises(ValueError, match="reference tree"):
         ta.attn_fn(x, x, x, False, None)
 
 
-def test_op_level_rejects_deterministic_mode_and_bad_shapes():
+def test_op_level_mode_and_shape_errors():
     x = torch.zeros(8, 1, 64)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="device"):
         ta.hierarchical_attention(x, x[:7], x, num_heads=2, mode="deterministic")
+    with pytest.raises(ValueError, match="mode"):
+        ta.hierarchical_attention(x, x[:7], x, num_heads=2, mode="exact")
     with pytest.raises(ValueError):
         ta.hierarchical_attention(x, x[:5], x, num_heads=2)
     with pytest.raises(ValueError):
         ta.hierarchical_attention(x, x[:7], x, num_heads=3)
+    with pytest.raises(ValueError, match="num_samples"):
+        ta.hierarchical_attention(x, x[:7], x, num_heads=2, num_samples=None)
+
+
+def test_deterministic_entry_points_validate_before_launching():
+    lib = _lib.load()
+    # non-power-of-two and oversized leaf counts are refused with a message, nothing is launched
+    assert lib.ta_det_weights(None, 11, None, 12, 0, 1, 12, 0, None) == 2
+    assert b"2^T" in lib.ta_last_error()
+    assert lib.ta_det_grad(None, 65535, None, None, 65536, 1, 65536, 0, None) == 2
+    assert lib.ta_det_weights(None, 15, None, 16, 0, 1, 16, 0, None) == 0  # no rows: nothing to do
+    assert lib.ta_det_weights(None, 3, None, 16, 16, 16, 16, 0, None) == 1  # row stride too small
+    ks = (ctypes.c_int64 * 3)(0, 0, 0)
+    assert lib.ta_haar_keys(_lib.TA_BF16, None, ks, None, 1, 1, 32, 12, None) == 1
 
 
 def test_cpu_tensors_are_rejected_not_computed():

@@ -66,6 +66,10 @@ EXPORTS = (
     "ta_leaf_backward",
     "ta_tree_backward",
     "ta_backward",
+    "ta_det_weights",
+    "ta_det_grad",
+    "ta_haar_keys",
+    "ta_haar_keys_adjoint",
 )
 
 _lock = threading.Lock()
@@ -104,6 +108,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_forward.argtypes = [P, vp, vp, vp, vp, ctypes.c_uint64, vp, vp, vp, vp, vp]
     lib.ta_backward.restype = ctypes.c_int
     lib.ta_backward.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    i64 = ctypes.c_int64
+    lib.ta_det_weights.restype = ctypes.c_int
+    lib.ta_det_weights.argtypes = [vp, i64, vp, i64, i64, i64, i64, ctypes.c_int, vp]
+    lib.ta_det_grad.restype = ctypes.c_int
+    lib.ta_det_grad.argtypes = [vp, i64, vp, vp, i64, i64, i64, ctypes.c_int, vp]
+    lib.ta_haar_keys.restype = ctypes.c_int
+    lib.ta_haar_keys.argtypes = [ctypes.c_int, vp, i64p, vp, i64, i64, i64, i64, vp]
+    lib.ta_haar_keys_adjoint.restype = ctypes.c_int
+    lib.ta_haar_keys_adjoint.argtypes = [ctypes.c_int, vp, vp, i64p, i64, i64, i64, i64, vp]
 
 
 def load() -> ctypes.CDLL:

@@ -21,7 +21,13 @@ from typing import Callable
 
 import torch
 
-from .function import StochasticTreeAttention, TreeAttentionFunction, TreeOptions
+from .function import (
+    DeterministicAdapterAttention,
+    DeterministicTreeAttention,
+    StochasticTreeAttention,
+    TreeAttentionFunction,
+    TreeOptions,
+)
 
 NUM_SAMPLES_ENV_VAR = "TREEATTN_NUM_SAMPLES"
 BRANCHING_ENV_VAR = "TREEATTN_BRANCHING"
@@ -92,15 +98,17 @@ def hierarchical_attention(
     seed: int = 0,
     uniforms: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Stochastic hierarchical attention, reference signature.
+    """Hierarchical attention, reference signature (``_tree_mha.py:324-413``).
 
-    ``uniforms`` (optional, float32 ``(B, L, H, S, T, 2)``, contiguous)
-    replaces the Gumbel noise stream; without it the counter RNG with
-    ``seed`` supplies it, so equal inputs give equal outputs.
+    ``mode="stochastic"``: ``uniforms`` (optional, float32 ``(B, L, H, S, T,
+    2)``, contiguous) replaces the Gumbel noise stream; without it the counter
+    RNG with ``seed`` supplies it, so equal inputs give equal outputs.
+    ``mode="deterministic"``: exact attention over every leaf, weights
+    ``(L, B, H, N)`` (``_tree_mha.py:271-321``); ``N`` a power of two.
     """
-    if mode != "stochastic":
-        raise NotImplementedError("deterministic (exact) tree attention is not implemented by this backend")
-    if num_samples is None:
+    if mode not in ("stochastic", "deterministic"):
+        raise ValueError(f"mode must be 'stochastic' or 'deterministic', got {mode!r}")
+    if mode == "stochastic" and num_samples is None:
         raise ValueError("num_samples must be provided for stochastic mode.")
     if query.dim() != 3 or value.dim() != 3:
         raise ValueError("query and value must have shape (L, B, E) and (N, B, E)")
@@ -116,6 +124,9 @@ def hierarchical_attention(
     q = query.reshape(L, B, H, D)
     k = key.reshape(max(K, 0), B, H, D) if K > 0 else key.new_empty((0, B, H, D))
     v = value.reshape(N, B, H, D)
+    if mode == "deterministic":
+        out, weights = DeterministicTreeAttention.apply(q, k, v, bool(is_causal))
+        return out.reshape(L, B, E), weights
     out, weights = StochasticTreeAttention.apply(q, k, v, num_samples, block_size, max_logit, is_causal, seed,
                                                  uniforms)
     return out.reshape(L, B, E), weights
@@ -159,17 +170,25 @@ def tree_attention(
 def attn_fn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, softmax_scale: float | None) -> torch.Tensor:
     """attn-bench kernel: ``(B, S, H, D)`` in, same shape and dtype out.
 
-    Like treeattn-cuda's adapter (``baselines/treeattn_cuda.py:24-59``) the
-    stochastic mode needs ``TREEATTN_NUM_SAMPLES``; the tree shape comes from
-    ``TREEATTN_BRANCHING`` / ``TREEATTN_LEAF_BLOCK`` / ``TREEATTN_TREE_MODE``
-    (default: the reference tree).  ``softmax_scale`` is used inside leaf
-    blocks only (the reference ignores it, ``baselines/treeattn_torch.py:53``;
-    at ``leaf_block=1`` it has no effect).
+    Like treeattn-torch's adapter (``baselines/treeattn_torch.py:48-90``):
+    ``TREEATTN_NUM_SAMPLES`` set -> stochastic mode with that many paths,
+    unset (or ``0``) -> deterministic (exact) mode on the reference tree (Haar
+    node keys of ``k``, ``S`` a power of two).  The stochastic tree shape
+    comes from ``TREEATTN_BRANCHING`` / ``TREEATTN_LEAF_BLOCK`` /
+    ``TREEATTN_TREE_MODE`` (default: the reference tree).  ``softmax_scale``
+    is used inside leaf blocks only (the reference ignores it,
+    ``baselines/treeattn_torch.py:53``; at ``leaf_block=1`` it has no effect).
     """
     num_samples = resolve_num_samples()
-    if num_samples is None:
-        raise ValueError(f"this backend requires {NUM_SAMPLES_ENV_VAR} to be set (stochastic mode)")
     cfg = resolve_tree_config()
+    if num_samples is None:
+        if (cfg["branching"], cfg["leaf_block"], cfg["tree_mode"]) != (2, 1, "compat"):
+            raise ValueError("deterministic mode (TREEATTN_NUM_SAMPLES unset) runs on the reference tree only: "
+                             "branching 2, leaf block 1, compat keys")
+        S = q.shape[1]
+        if S < 2 or S & (S - 1):
+            raise ValueError(f"deterministic tree attention requires power-of-two seqlen, got {S}")
+        return DeterministicAdapterAttention.apply(q, k, v, bool(causal))
     return tree_attention(q, k, v, causal, softmax_scale, num_samples=num_samples, **cfg)
 
 

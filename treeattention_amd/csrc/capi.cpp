@@ -336,4 +336,74 @@ int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v
                        "tree_backward");
 }
 
+// ---- deterministic mode
+
+static int det_depth(int64_t N, int* T) {
+  if (N < 2 || N > TA_DET_MAX_LEAVES || (N & (N - 1)))
+    return fail(TA_ERR_UNSUPPORTED, "deterministic mode needs N = 2^T leaves with 2 <= N <= %d (got %lld)",
+                TA_DET_MAX_LEAVES, (long long)N);
+  int t = 0;
+  while ((1LL << t) < N) ++t;
+  *T = t;
+  return TA_OK;
+}
+
+int ta_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw, int64_t rows, int64_t L, int64_t N, int causal,
+                   void* stream) {
+  int T = 0;
+  const int rc = det_depth(N, &T);
+  if (rc) return rc;
+  if (rows < 0 || L < 1 || rows % L) return fail(TA_ERR_INVALID, "rows must be a multiple of L >= 1");
+  if (ldx < N - 1 || ldw < N) return fail(TA_ERR_INVALID, "row strides too small (ldx >= N-1, ldw >= N)");
+  if (rows > 0 && (!X || !W)) return fail(TA_ERR_INVALID, "NULL device pointer");
+  if (rows >= ((int64_t)1 << 31)) return fail(TA_ERR_UNSUPPORTED, "too many rows");
+  if (rows == 0) return ok();
+  return launch_status(launch_det_weights(X, ldx, W, ldw, rows, (int)L, (int)N, T, causal != 0, (hipStream_t)stream),
+                       "det_weights");
+}
+
+int ta_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows, int64_t N,
+                int causal, void* stream) {
+  int T = 0;
+  const int rc = det_depth(N, &T);
+  if (rc) return rc;
+  if (rows < 0) return fail(TA_ERR_INVALID, "rows must be >= 0");
+  if (ldx < N - 1 || ldw < N) return fail(TA_ERR_INVALID, "row strides too small (ldx >= N-1, ldw >= N)");
+  if (rows > 0 && (!XG || !W || !dW)) return fail(TA_ERR_INVALID, "NULL device pointer");
+  if (rows >= ((int64_t)1 << 31)) return fail(TA_ERR_UNSUPPORTED, "too many rows");
+  if (rows == 0) return ok();
+  return launch_status(launch_det_grad(XG, ldx, W, dW, ldw, rows, (int)N, T, causal != 0, (hipStream_t)stream),
+                       "det_grad");
+}
+
+static int haar_check(int dtype, const void* a, const void* b, const int64_t* s, int64_t B, int64_t H, int64_t D,
+                      int64_t N) {
+  if (dtype != TA_F32 && dtype != TA_BF16 && dtype != TA_F16) return fail(TA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (B < 1 || H < 1 || N < 2 || (N & (N - 1))) return fail(TA_ERR_INVALID, "need B, H >= 1 and N = 2^T >= 2");
+  if (D < 4 || D % 4) return fail(TA_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 (got %lld)", (long long)D);
+  if (!a || !b || !s) return fail(TA_ERR_INVALID, "NULL pointer");
+  if (((uintptr_t)a & 15) || ((uintptr_t)b & 15)) return fail(TA_ERR_INVALID, "pointers must be 16-byte aligned");
+  if (N * B * H * D >= ((int64_t)1 << 40)) return fail(TA_ERR_UNSUPPORTED, "tensor too large");
+  return TA_OK;
+}
+
+int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, int64_t B, int64_t H, int64_t D,
+                 int64_t N, void* stream) {
+  const int rc = haar_check(dtype, k, out, k_strides, B, H, D, N);
+  if (rc) return rc;
+  return launch_status(
+      launch_haar_keys(dtype, k, k_strides, out, (int)B, (int)H, (int)D, (int)N, (hipStream_t)stream), "haar_keys");
+}
+
+int ta_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* dk_strides, int64_t B, int64_t H,
+                         int64_t D, int64_t N, void* stream) {
+  const int rc = haar_check(dtype, dkey, dk, dk_strides, B, H, D, N);
+  if (rc) return rc;
+  int T = 0;
+  while ((1LL << T) < N) ++T;
+  return launch_status(launch_haar_keys_adjoint(dtype, dkey, dk, dk_strides, (int)B, (int)H, (int)D, (int)N, T,
+                                                (hipStream_t)stream),
+                       "haar_keys_adjoint");
+}
+
 }  // extern "C"

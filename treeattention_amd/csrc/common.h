@@ -20,6 +20,7 @@ constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 cov
 constexpr int kMaxSamples = 64;   // one wavefront lane per sample
 constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
 constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
+constexpr int kDetMaxLeaves = TA_DET_MAX_LEAVES;  // deterministic mode: leaves per row held in LDS
 
 // Tree geometry.  Child summaries are stored level-major: level lam (1..T)
 // holds b^lam rows starting at off[lam], padded with zero rows to a multiple

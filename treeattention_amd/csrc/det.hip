@@ -1,0 +1,269 @@
+// Deterministic (exact) tree attention on the reference tree: binary, one
+// token per leaf, heap-ordered node keys (_tree_mha.py:271-321).
+//
+// Query l reaches leaf n with probability prod_d sigma(+-x), x = q_l . k_node
+// over the n's root-to-leaf path (left child: sigma(x), right: sigma(-x),
+// _tree_mha.py:287-306).  Non-causal weights are those probabilities; causal
+// weights are their softmax over the leaves n <= l (:308-314).  The dense
+// products (node logits X = Q K^T, out = W V and the gradient products) are
+// plain batched GEMMs; these kernels do the tree-structured parts per row
+// (one (batch, head, query) row per workgroup):
+//   det_weights_kernel: X row -> leaf log-probabilities by a top-down level
+//     recursion in LDS (lp[2i + c] = lp[i] + logsig(+-x), logsig(-x) =
+//     logsig(x) - x), then exp or the causal softmax;
+//   det_grad_kernel:    W, dW rows -> dlogw = W (dW - delta) (delta = sum W dW
+//     when causal, 0 otherwise), bottom-up subtree sums A, and the node-logit
+//     gradient G = sigma(-x) A_left - sigma(x) A_right, written over X;
+//   haar_keys_kernel / haar_keys_adjoint_kernel: the heap-ordered Haar node
+//     keys of the attn-bench adapter (_treeattn_common.py:54-86) and the
+//     transpose of that linear map.
+#include "launch.h"
+
+namespace ta {
+
+constexpr int kDetThreads = 1024;
+constexpr int kDetPer = kDetMaxLeaves / 2 / kDetThreads;  // level entries per thread
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red[i];
+  return s;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = -__builtin_inff();
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = fmaxf(s, red[i]);
+  return s;
+}
+
+// grid: rows (B*H*L), block kDetThreads, dynamic LDS N floats.
+__global__ __launch_bounds__(kDetThreads) void det_weights_kernel(const float* __restrict__ X, int64_t ldx,
+                                                                  float* __restrict__ W, int64_t ldw, int L, int N,
+                                                                  int T, int causal) {
+  extern __shared__ float lp[];
+  __shared__ float red[kDetThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int l = (int)(r % L);
+  const int tid = threadIdx.x;
+  const float* x = X + r * ldx;
+  if (tid == 0) lp[0] = 0.f;
+  __syncthreads();
+  for (int d = 0; d < T; ++d) {
+    const int nd = 1 << d;
+    float a[kDetPer], xs[kDetPer];
+#pragma unroll
+    for (int j = 0; j < kDetPer; ++j) {
+      const int i = tid + kDetThreads * j;
+      if (i < nd) {
+        a[j] = lp[i];
+        xs[j] = x[nd - 1 + i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kDetPer; ++j) {
+      const int i = tid + kDetThreads * j;
+      if (i < nd) {
+        const float ls = logsig(xs[j]);
+        lp[2 * i] = a[j] + ls;
+        lp[2 * i + 1] = a[j] + ls - xs[j];
+      }
+    }
+    __syncthreads();
+  }
+  float* w = W + r * ldw;
+  if (causal) {
+    float m = -__builtin_inff();
+    for (int n = tid; n <= l && n < N; n += kDetThreads) m = fmaxf(m, lp[n]);
+    m = block_max(m, red);
+    float s = 0.f;
+    for (int n = tid; n <= l && n < N; n += kDetThreads) s += expf(lp[n] - m);
+    s = block_sum(s, red);
+    const float inv = 1.f / s;
+    for (int n = tid; n < N; n += kDetThreads) w[n] = n <= l ? expf(lp[n] - m) * inv : 0.f;
+  } else {
+    for (int n = tid; n < N; n += kDetThreads) w[n] = expf(lp[n]);
+  }
+}
+
+// grid: rows, block kDetThreads, dynamic LDS N floats.  G overwrites X.
+__global__ __launch_bounds__(kDetThreads) void det_grad_kernel(float* __restrict__ XG, int64_t ldx,
+                                                               const float* __restrict__ W, const float* __restrict__ dW,
+                                                               int64_t ldw, int N, int T, int causal) {
+  extern __shared__ float A[];
+  __shared__ float red[kDetThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* w = W + r * ldw;
+  const float* dw = dW + r * ldw;
+  float* xg = XG + r * ldx;
+  float delta = 0.f;
+  if (causal) {
+    float s = 0.f;
+    for (int n = tid; n < N; n += kDetThreads) s += w[n] * dw[n];
+    delta = block_sum(s, red);
+  }
+  for (int n = tid; n < N; n += kDetThreads) A[n] = w[n] * (dw[n] - delta);
+  __syncthreads();
+  for (int d = T - 1; d >= 0; --d) {
+    const int nd = 1 << d;
+    float al[kDetPer], ar[kDetPer], xs[kDetPer];
+#pragma unroll
+    for (int j = 0; j < kDetPer; ++j) {
+      const int i = tid + kDetThreads * j;
+      if (i < nd) {
+        al[j] = A[2 * i];
+        ar[j] = A[2 * i + 1];
+        xs[j] = xg[nd - 1 + i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kDetPer; ++j) {
+      const int i = tid + kDetThreads * j;
+      if (i < nd) {
+        const float s = 1.f / (1.f + expf(-xs[j]));
+        xg[nd - 1 + i] = (1.f - s) * al[j] - s * ar[j];
+        A[i] = al[j] + ar[j];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Heap node m of an N-leaf binary tree (p = m + 1, w = lowest set bit of p):
+// key = (mean of k[p-w, p) - mean of k[p, p+w)) / 2, the in-order Haar
+// coefficient p of the keys read in heap order (_treeattn_common.py:70-86,
+// _tree_mha.py:104,119).  Output (K, B, H, D) float; one thread per
+// (m, b, h, 4 dims).
+template <typename E>
+__global__ __launch_bounds__(256) void haar_keys_kernel(const E* __restrict__ k, int64_t sb, int64_t sl, int64_t sh,
+                                                        float* __restrict__ out, int B, int H, int D, int N) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int D4 = D / 4;
+  const int64_t total = (int64_t)(N - 1) * B * H * D4;
+  if (e >= total) return;
+  const int d0 = (int)(e % D4) * 4;
+  const int64_t mbh = e / D4;
+  const int h = (int)(mbh % H);
+  const int64_t mb = mbh / H;
+  const int bb = (int)(mb % B);
+  const int m = (int)(mb / B);
+  const int p = m + 1, w = p & (-p);
+  const E* base = k + bb * sb + h * sh + d0;
+  float sl_[4] = {0, 0, 0, 0}, sr_[4] = {0, 0, 0, 0};
+  for (int t = 0; t < w; ++t) {
+    const E* a = base + (int64_t)(p - w + t) * sl;
+    const E* c = base + (int64_t)(p + t) * sl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sl_[i] += tof(a[i]);
+      sr_[i] += tof(c[i]);
+    }
+  }
+  const float f = 0.5f / (float)w;
+  float* o = out + (((int64_t)m * B + bb) * H + h) * D + d0;
+  *(float4*)o = make_float4((sl_[0] - sr_[0]) * f, (sl_[1] - sr_[1]) * f, (sl_[2] - sr_[2]) * f,
+                            (sl_[3] - sr_[3]) * f);
+}
+
+// dk[b, t, h, :] = sum over the levels l of +-dkey[m_l] / 2^(l+1): at level l
+// leaf t lies in the left (+) or right (-) span of exactly one coefficient,
+// p_l = (t >> (l+1) << (l+1)) + 2^l.  One thread per (t, b, h, 4 dims).
+template <typename E>
+__global__ __launch_bounds__(256) void haar_keys_adjoint_kernel(const float* __restrict__ dkey, E* __restrict__ dk,
+                                                                int64_t sb, int64_t sl, int64_t sh, int B, int H, int D,
+                                                                int N, int T) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int D4 = D / 4;
+  const int64_t total = (int64_t)N * B * H * D4;
+  if (e >= total) return;
+  const int d0 = (int)(e % D4) * 4;
+  const int64_t tbh = e / D4;
+  const int h = (int)(tbh % H);
+  const int64_t tb = tbh / H;
+  const int bb = (int)(tb % B);
+  const int t = (int)(tb / B);
+  float acc[4] = {0, 0, 0, 0};
+  for (int l = 0; l < T; ++l) {
+    const int p = ((t >> (l + 1)) << (l + 1)) + (1 << l);
+    const float f = (((t >> l) & 1) ? -0.5f : 0.5f) / (float)(1 << l);
+    const float4 g = *(const float4*)(dkey + (((int64_t)(p - 1) * B + bb) * H + h) * D + d0);
+    acc[0] += f * g.x;
+    acc[1] += f * g.y;
+    acc[2] += f * g.z;
+    acc[3] += f * g.w;
+  }
+  E* o = dk + bb * sb + (int64_t)t * sl + h * sh + d0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (E)acc[i];
+}
+
+hipError_t launch_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw, int64_t rows, int L, int N, int T,
+                              int causal, hipStream_t st) {
+  const int smem = N * 4;
+  hipError_t e = hipFuncSetAttribute((const void*)det_weights_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(det_weights_kernel, dim3((unsigned)rows), dim3(kDetThreads), smem, st, X, ldx, W, ldw, L, N, T,
+                     causal);
+  return hipGetLastError();
+}
+
+hipError_t launch_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows, int N,
+                           int T, int causal, hipStream_t st) {
+  const int smem = N * 4;
+  hipError_t e = hipFuncSetAttribute((const void*)det_grad_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(det_grad_kernel, dim3((unsigned)rows), dim3(kDetThreads), smem, st, XG, ldx, W, dW, ldw, N, T,
+                     causal);
+  return hipGetLastError();
+}
+
+template <typename E>
+static hipError_t haar_keys_t(const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
+                              hipStream_t st) {
+  const int64_t total = (int64_t)(N - 1) * B * H * (D / 4);
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(haar_keys_kernel<E>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (const E*)k, ks[0],
+                     ks[1], ks[2], out, B, H, D, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
+                            hipStream_t st) {
+  switch (dtype) {
+    case TA_F32: return haar_keys_t<float>(k, ks, out, B, H, D, N, st);
+    case TA_BF16: return haar_keys_t<bf16>(k, ks, out, B, H, D, N, st);
+    default: return haar_keys_t<f16>(k, ks, out, B, H, D, N, st);
+  }
+}
+
+template <typename E>
+static hipError_t haar_adj_t(const float* dkey, void* dk, const int64_t* ks, int B, int H, int D, int N, int T,
+                             hipStream_t st) {
+  const int64_t total = (int64_t)N * B * H * (D / 4);
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(haar_keys_adjoint_kernel<E>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, dkey,
+                     (E*)dk, ks[0], ks[1], ks[2], B, H, D, N, T);
+  return hipGetLastError();
+}
+
+hipError_t launch_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* ks, int B, int H, int D,
+                                    int N, int T, hipStream_t st) {
+  switch (dtype) {
+    case TA_F32: return haar_adj_t<float>(dkey, dk, ks, B, H, D, N, T, st);
+    case TA_BF16: return haar_adj_t<bf16>(dkey, dk, ks, B, H, D, N, T, st);
+    default: return haar_adj_t<f16>(dkey, dk, ks, B, H, D, N, T, st);
+  }
+}
+
+}  // namespace ta

@@ -42,6 +42,16 @@ hipError_t launch_leaf_bwd(const Plan& P, const void* q, const void* k, const vo
 hipError_t launch_tree_bwd(const Plan& P, const void* q, const float* weights, const char* rec,
                            void* dq, void* dk, char* ws, hipStream_t st);
 
+// det.hip (deterministic mode)
+hipError_t launch_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw, int64_t rows, int L, int N, int T,
+                              int causal, hipStream_t st);
+hipError_t launch_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows, int N,
+                           int T, int causal, hipStream_t st);
+hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
+                            hipStream_t st);
+hipError_t launch_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* ks, int B, int H, int D,
+                                    int N, int T, hipStream_t st);
+
 // Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
 // variant fits in 160 KiB.
 int leaf_fwd_smem(const Plan& P);

@@ -1,4 +1,7 @@
-"""Autograd Function over the HIP library.
+"""Autograd Functions over the HIP library.
+
+``DeterministicTreeAttention`` / ``DeterministicAdapterAttention`` run the
+reference's exact mode (``_tree_mha.py:271-321``); see the section below.
 
 ``TreeAttentionFunction`` is the MI355X counterpart of treeattn-cuda's
 ``_StochasticNonCausalTreeAttention`` (``_autograd.py:645-860``): the forward
@@ -289,6 +292,165 @@ class StochasticTreeAttention(torch.autograd.Function):
         q, k, v, weights, record = ctx.saved_tensors
         dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, ctx.opts)
         return (dq, dk, dv) + nones
+
+
+# ---------------------------------------------------------------------------
+# Deterministic (exact) mode on the reference tree (_tree_mha.py:271-321).
+# The node logits X = Q K^T and the products out = W V, dW = dout V^T,
+# dq = G K, dK = G^T Q, dv = W^T dout are plain batched GEMMs (the BLAS
+# library behind torch.matmul); the tree recursion over every row (weights,
+# and the node-logit gradient G) runs in the library's HIP kernels.  Memory is
+# that of the reference's mode: the (L, B, H, N) weights it returns, plus the
+# logits.
+
+
+def _bh(t: torch.Tensor) -> torch.Tensor:
+    """(L, B, H, D) -> contiguous float32 (B, H, L, D)."""
+    return t.permute(1, 2, 0, 3).float().contiguous()
+
+
+def _on_device(*ts) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("tree attention runs on HIP device tensors; got a tensor on " + str(t.device))
+
+
+def det_forward(q, k, v, causal: bool):
+    """``q (L,B,H,D)``, node keys ``k (N-1,B,H,D)``, ``v (N,B,H,D)`` -> ``(out (L,B,H,D)
+    in v's dtype, W (B,H,L,N) float32)``."""
+    _on_device(q, k, v)
+    lib = _lib.load()
+    L, B, H, _ = q.shape
+    N = v.shape[0]
+    qf, kf = _bh(q), _bh(k)
+    X = torch.matmul(qf, kf.transpose(-1, -2).contiguous())  # (B, H, L, N-1)
+    W = torch.empty((B, H, L, N), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ta_det_weights(X.data_ptr(), N - 1, W.data_ptr(), N, B * H * L, L, N, int(bool(causal)),
+                                      _stream(q.device)))
+    out = torch.matmul(W.to(v.dtype), v.permute(1, 2, 0, 3).contiguous())  # weights cast to v's dtype (:318)
+    return out.permute(2, 0, 1, 3), W
+
+
+def det_backward(q, k, v, W, grad_out, causal: bool):
+    """Gradients ``(dq, dk, dv)`` of ``det_forward`` (same layouts and dtypes as the inputs)."""
+    lib = _lib.load()
+    L, B, H, _ = q.shape
+    N = v.shape[0]
+    qf, kf, vf, gf = _bh(q), _bh(k), _bh(v), _bh(grad_out)
+    X = torch.matmul(qf, kf.transpose(-1, -2).contiguous())  # node logits, overwritten by G
+    dW = torch.matmul(gf, vf.transpose(-1, -2).contiguous())  # (B, H, L, N)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ta_det_grad(X.data_ptr(), N - 1, W.data_ptr(), dW.data_ptr(), N, B * H * L, N,
+                                   int(bool(causal)), _stream(q.device)))
+    del dW
+    G = X
+    dq = torch.matmul(G, kf)
+    dk = torch.matmul(G.transpose(-1, -2), qf)
+    dv = torch.matmul(W.transpose(-1, -2), gf)
+    back = lambda t, like: t.permute(2, 0, 1, 3).to(like.dtype)  # noqa: E731
+    return back(dq, q), back(dk, k), back(dv, v)
+
+
+def _edge_forward(q, v):
+    """``N <= 1`` outputs of the reference (``_tree_mha.py:367-372``)."""
+    if v.shape[0] == 0:
+        return torch.zeros_like(q), torch.empty((*q.shape[:-1], 0), device=q.device, dtype=q.dtype)
+    return v.expand(q.shape[0], -1, -1, -1).contiguous(), torch.ones((*q.shape[:-1], 1), device=q.device,
+                                                                       dtype=q.dtype)
+
+
+def _edge_backward(q, k, v, grad_out):
+    dv = torch.zeros_like(v)
+    if v.shape[0] == 1:
+        dv[0] = grad_out.float().sum(dim=0).to(v.dtype)
+    return torch.zeros_like(q), torch.zeros_like(k), dv
+
+
+class DeterministicTreeAttention(torch.autograd.Function):
+    """Exact tree attention of the reference's ``mode="deterministic"``.
+
+    ``apply(q (L,B,H,D), k (N-1,B,H,D) heap-ordered node keys, v (N,B,H,D),
+    is_causal=False) -> (out (L,B,H,D), weights (L,B,H,N) float32)`` with
+    ``_deterministic_attention``'s weights (``_tree_mha.py:271-321``): the
+    product of the path's sigmoids, or with ``is_causal`` their softmax over
+    leaves ``n <= l``.  Gradients ``(dq, dk, dv, None)``; the returned weights
+    are not differentiable.  ``N`` must be a power of two.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal=False):
+        ctx.num_leaves = v.shape[0]
+        if v.shape[0] <= 1:
+            out, weights = _edge_forward(q, v)
+            ctx.save_for_backward(q, k, v)
+            ctx.mark_non_differentiable(weights)
+            return out, weights
+        out, W = det_forward(q, k, v, is_causal)
+        ctx.save_for_backward(q, k, v, W)
+        ctx.causal = bool(is_causal)
+        weights = W.permute(2, 0, 1, 3)
+        ctx.mark_non_differentiable(weights)
+        return out, weights
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_weights):
+        del grad_weights
+        if ctx.num_leaves <= 1:
+            return _edge_backward(*ctx.saved_tensors, grad_out) + (None,)
+        q, k, v, W = ctx.saved_tensors
+        return det_backward(q, k, v, W, grad_out, ctx.causal) + (None,)
+
+
+def haar_node_keys(k: torch.Tensor) -> torch.Tensor:
+    """Heap-ordered Haar node keys ``(N-1, B, H, D)`` float32 of bshd keys ``k (B, N, H, D)``,
+    what the reference adapter feeds the op (``_treeattn_common.py:54-86``, read in heap order)."""
+    _on_device(k)
+    lib = _lib.load()
+    B, N, H, D = k.shape
+    k = _prep(k)
+    out = torch.empty((N - 1, B, H, D), device=k.device, dtype=torch.float32)
+    ks = (ctypes.c_int64 * 3)(*_strides(k, "bshd"))
+    with torch.cuda.device(k.device):
+        _lib.check(lib.ta_haar_keys(_DTYPES[k.dtype], k.data_ptr(), ks, out.data_ptr(), B, H, D, N,
+                                    _stream(k.device)))
+    return out
+
+
+def haar_node_keys_adjoint(dkey: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """``dk (B, N, H, D)`` in ``like``'s dtype from node-key gradients ``dkey (N-1, B, H, D)``."""
+    lib = _lib.load()
+    B, N, H, D = like.shape
+    dk = torch.empty((B, N, H, D), device=like.device, dtype=like.dtype)
+    ks = (ctypes.c_int64 * 3)(*_strides(dk, "bshd"))
+    dkey = dkey.float().contiguous()
+    with torch.cuda.device(like.device):
+        _lib.check(lib.ta_haar_keys_adjoint(_DTYPES[like.dtype], dkey.data_ptr(), dk.data_ptr(), ks, B, H, D, N,
+                                            _stream(like.device)))
+    return dk
+
+
+class DeterministicAdapterAttention(torch.autograd.Function):
+    """The attn-bench adapter's deterministic path (``baselines/treeattn_torch.py:48-90`` with
+    ``TREEATTN_NUM_SAMPLES`` unset): bshd ``q, k, v (B, S, H, D)``, Haar node keys of ``k``,
+    exact tree attention; ``apply(q, k, v, causal) -> out (B, S, H, D)``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal):
+        kt = haar_node_keys(k)
+        ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
+        out, W = det_forward(ql, kt, vl, causal)
+        ctx.save_for_backward(q, k, v, kt, W)
+        ctx.causal = bool(causal)
+        return out.permute(1, 0, 2, 3).contiguous()
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, kt, W = ctx.saved_tensors
+        ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
+        dq, dkt, dv = det_backward(ql, kt, vl, W, grad_out.permute(1, 0, 2, 3), ctx.causal)
+        dk = haar_node_keys_adjoint(dkt, k)
+        return dq.permute(1, 0, 2, 3), dk, dv.permute(1, 0, 2, 3), None
 
 
 def record_views(q, k, v, opts: TreeOptions, record: torch.Tensor):
