@@ -1,9 +1,10 @@
-"""MI355X (gfx950) stochastic tree attention: hand-written HIP kernels behind a C ABI.
+"""MI355X (gfx950) tree attention: hand-written HIP kernels behind a C ABI.
 
 Entry points mirror the reference interfaces: ``hierarchical_attention``
-(treeattn-torch / treeattn-cuda op), ``StochasticTreeAttention`` (the
-autograd Function), ``attn_fn`` / ``adapter`` (attn-bench kernel contract),
-plus ``tree_attention`` for the generalized tree (branching, leaf blocks).
+(treeattn-torch / treeattn-cuda op, stochastic and deterministic modes),
+``StochasticTreeAttention`` / ``DeterministicTreeAttention`` (autograd
+Functions), ``attn_fn`` / ``adapter`` (attn-bench kernel contract), plus
+``tree_attention`` for the generalized tree (branching, leaf blocks).
 """
 
 from .api import (
@@ -15,9 +16,17 @@ from .api import (
     resolve_tree_config,
     tree_attention,
 )
-from .function import StochasticTreeAttention, TreeAttentionFunction, TreeOptions, tree_backward, tree_forward
+from .function import (
+    DeterministicTreeAttention,
+    StochasticTreeAttention,
+    TreeAttentionFunction,
+    TreeOptions,
+    tree_backward,
+    tree_forward,
+)
 
 __all__ = [
+    "DeterministicTreeAttention",
     "KernelAdapter",
     "StochasticTreeAttention",
     "TreeAttentionFunction",
