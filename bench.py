@@ -50,7 +50,13 @@ def parse():
     ap.add_argument("--phases-only", action="store_true", help="only run the per-phase loop (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM counters)")
-    return ap.parse_args()
+    ap.add_argument("--mode", default="stochastic", choices=("stochastic", "deterministic"),
+                    help="deterministic: the exact mode of the reference tree (adapter path, Haar keys) at the "
+                         "config's B, L, H, D, dtype and causality (default config C2)")
+    args = ap.parse_args()
+    if args.mode == "deterministic" and "--config" not in sys.argv:
+        args.config = "C2"
+    return args
 
 
 def tree_units(B, L, H, D, e, b, LB, S):
@@ -113,12 +119,92 @@ def cpu_baseline(cfg) -> dict:
                       f"(full {L}-token tree), {dt_s:.2f} s; scaled by 1/H to whole-query units"}
 
 
+def det_main(args) -> int:
+    """Deterministic mode on the reference tree: fwd+bwd of the adapter path (Haar keys, exact
+    weights over every leaf), plus the leaf-weight row kernel timed alone for its HBM roofline."""
+    import torch
+
+    from treeattention_amd import _lib
+    from treeattention_amd.function import DeterministicAdapterAttention
+
+    B, L, H, D, dts, _, _, _, causal, kind = CONFIGS[args.config]
+    dtype = getattr(torch, dts)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    q, k, v, do = (torch.randn((B, L, H, D), device=dev, dtype=dtype, generator=gen) for _ in range(4))
+    if kind == "scaled":
+        q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    for x in (q, k, v):
+        x.requires_grad_(True)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        DeterministicAdapterAttention.apply(q, k, v, causal).backward(do)
+
+    def fwd():
+        with torch.no_grad():
+            DeterministicAdapterAttention.apply(q, k, v, causal)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / n
+
+    for _ in range(args.warmup):
+        step()
+    step_ms = timed(step, args.steps)
+    fwd_ms = timed(fwd, args.steps)
+    # the leaf-weight row kernel alone: reads the N-1 node logits, writes the N weights of each row
+    lib = _lib.load()
+    rows, N = B * H * L, L
+    X = torch.randn((rows, N - 1), device=dev, dtype=torch.float32, generator=gen)
+    W = torch.empty((rows, N), device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    run = lambda: _lib.check(lib.ta_det_weights(X.data_ptr(), N - 1, W.data_ptr(), N, rows, L, N, int(causal),  # noqa: E731
+                                                stream))
+    run()
+    kern_ms = timed(run, max(3, args.steps))
+    alg_bytes = rows * (4 * (N - 1) + 4 * N)
+    achieved = alg_bytes / (kern_ms / 1e3) / 1e9
+    line = {
+        "metric": "deterministic tree-attn fwd+bwd ms & queries/s (reference tree, exact weights)",
+        "value": round(B * L / (step_ms / 1e3), 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(step_ms - fwd_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts.replace("bfloat16", "bf16").replace("float16", "fp16").replace("float32", "fp32"),
+        "data": "synthetic: q,k,v,dout ~ N(0,1) (torch.Generator seed 0)",
+        "config": {"workload": f"{args.config} shape, deterministic mode, reference tree (Haar keys)", "batch": B,
+                   "seq_len": L, "heads": H, "head_dim": D, "causal": causal},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "det_weights",
+                     "kernel_ms": round(kern_ms, 4)},
+    }
+    print(json.dumps(line))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported",
                           "n_gpus": args.gpus}))
         return 2
+    if args.mode == "deterministic":
+        return det_main(args)
     import torch
 
     import treeattention_amd as ta

@@ -499,6 +499,6 @@ constexpr int kQueryChunk = 256; // queries per bucketing chunk (one wavefront e
 // leaf-forward workgroup each, so the heavy low blocks of causal runs (a
 // block near the start is reachable from every later query) do not leave
 // one workgroup running long after the others.
-constexpr int kPieceFwd = 512;
+constexpr int kPieceFwd = 1024;
 
 }  // namespace ta

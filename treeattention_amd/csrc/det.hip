@@ -9,8 +9,8 @@
 // plain batched GEMMs; these kernels do the tree-structured parts per row
 // (one (batch, head, query) row per workgroup):
 //   det_weights_kernel: X row -> leaf log-probabilities by a top-down level
-//     recursion in LDS (lp[2i + c] = lp[i] + logsig(+-x), logsig(-x) =
-//     logsig(x) - x), then exp or the causal softmax;
+//     recursion (lp[2i + c] = lp[i] + logsig(+-x), logsig(-x) = logsig(x) - x),
+//     then exp or the causal softmax;
 //   det_grad_kernel:    W, dW rows -> dlogw = W (dW - delta) (delta = sum W dW
 //     when causal, 0 otherwise), bottom-up subtree sums A, and the node-logit
 //     gradient G = sigma(-x) A_left - sigma(x) A_right, written over X;
@@ -21,8 +21,15 @@
 
 namespace ta {
 
-constexpr int kDetThreads = 1024;
-constexpr int kDetPer = kDetMaxLeaves / 2 / kDetThreads;  // level entries per thread
+// One workgroup of kDetThreads per row.  The top kDetTop levels of the tree
+// (2^kDetTop subtree roots) run level by level through LDS; below them thread
+// t owns the subtree of root t, C = N >> kDetTop leaves, processed in chunks
+// of up to 16 leaves whose last four levels are a register recursion (no
+// barriers): the forward walks root -> chunk root -> leaves, the backward
+// leaves -> chunk root -> subtree root -> top levels.
+constexpr int kDetThreads = 256;
+constexpr int kDetTop = 8;  // 2^kDetTop == kDetThreads
+constexpr int kDetChunks = kDetMaxLeaves / kDetThreads / 16;  // chunks per thread at most
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
@@ -45,97 +52,161 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return s;
 }
 
-// grid: rows (B*H*L), block kDetThreads, dynamic LDS N floats.
+// Heap index of the node at depth dd on the path to leaf n of a depth-T tree.
+__device__ __forceinline__ int path_node(int dd, int n, int T) { return (1 << dd) - 1 + (n >> (T - dd)); }
+
+// grid: rows (B*H*L), block kDetThreads, dynamic LDS N floats when causal.
 __global__ __launch_bounds__(kDetThreads) void det_weights_kernel(const float* __restrict__ X, int64_t ldx,
                                                                   float* __restrict__ W, int64_t ldw, int L, int N,
                                                                   int T, int causal) {
-  extern __shared__ float lp[];
+  extern __shared__ float lp[];  // causal: the row's leaf log-probabilities
+  __shared__ float top[2][kDetThreads];
   __shared__ float red[kDetThreads / 64];
   const int64_t r = blockIdx.x;
   const int l = (int)(r % L);
   const int tid = threadIdx.x;
   const float* x = X + r * ldx;
-  if (tid == 0) lp[0] = 0.f;
+  float* w = W + r * ldw;
+  const int tb = min(T, kDetTop), c = T - tb, C = 1 << c;
+  const int cl = min(c, 4), nchunk = C >> cl;
+  const bool vec = (reinterpret_cast<uintptr_t>(w) & 15) == 0;  // 16-byte row stores
+
+  int cur = 0;
+  if (tid == 0) top[0][0] = 0.f;
   __syncthreads();
-  for (int d = 0; d < T; ++d) {
+  for (int d = 0; d < tb; ++d) {
     const int nd = 1 << d;
-    float a[kDetPer], xs[kDetPer];
-#pragma unroll
-    for (int j = 0; j < kDetPer; ++j) {
-      const int i = tid + kDetThreads * j;
-      if (i < nd) {
-        a[j] = lp[i];
-        xs[j] = x[nd - 1 + i];
-      }
+    if (tid < nd) {
+      const float a = top[cur][tid], xv = x[nd - 1 + tid];
+      const float ls = logsig(xv);
+      top[cur ^ 1][2 * tid] = a + ls;
+      top[cur ^ 1][2 * tid + 1] = a + ls - xv;
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kDetPer; ++j) {
-      const int i = tid + kDetThreads * j;
-      if (i < nd) {
-        const float ls = logsig(xs[j]);
-        lp[2 * i] = a[j] + ls;
-        lp[2 * i + 1] = a[j] + ls - xs[j];
-      }
-    }
+    cur ^= 1;
     __syncthreads();
   }
-  float* w = W + r * ldw;
+  float mx = -__builtin_inff();
+  if (tid < (1 << tb)) {
+    const float root = top[cur][tid];
+    for (int j = 0; j < nchunk; ++j) {
+      const int base = tid * C + (j << cl);
+      float p = root;
+      for (int dd = tb; dd < T - cl; ++dd) {  // subtree root -> chunk root
+        const float xv = x[path_node(dd, base, T)];
+        const float ls = logsig(xv);
+        p += ((base >> (T - 1 - dd)) & 1) ? ls - xv : ls;
+      }
+      float a[16];
+      a[0] = p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e < cl) {
+          const int n0 = path_node(T - cl + e, base, T);
+#pragma unroll
+          for (int i = (1 << e) - 1; i >= 0; --i) {  // descending: a[2i], a[2i+1] overwrite nothing unread
+            const float xv = x[n0 + i];
+            const float ls = logsig(xv);
+            a[2 * i + 1] = a[i] + ls - xv;
+            a[2 * i] = a[i] + ls;
+          }
+        }
+      }
+      const int m = 1 << cl;
+      if (causal) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < m) {
+            lp[base + i] = a[i];
+            if (base + i <= l) mx = fmaxf(mx, a[i]);
+          }
+      } else if (m == 16 && vec) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+          *(float4*)(w + base + i) = make_float4(expf(a[i]), expf(a[i + 1]), expf(a[i + 2]), expf(a[i + 3]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < m) w[base + i] = expf(a[i]);
+      }
+    }
+  }
   if (causal) {
-    float m = -__builtin_inff();
-    for (int n = tid; n <= l && n < N; n += kDetThreads) m = fmaxf(m, lp[n]);
-    m = block_max(m, red);
+    mx = block_max(mx, red);  // includes a barrier: lp is complete
     float s = 0.f;
-    for (int n = tid; n <= l && n < N; n += kDetThreads) s += expf(lp[n] - m);
+    for (int n = tid; n <= l && n < N; n += kDetThreads) s += expf(lp[n] - mx);
     s = block_sum(s, red);
     const float inv = 1.f / s;
-    for (int n = tid; n < N; n += kDetThreads) w[n] = n <= l ? expf(lp[n] - m) * inv : 0.f;
-  } else {
-    for (int n = tid; n < N; n += kDetThreads) w[n] = expf(lp[n]);
+    for (int n = tid; n < N; n += kDetThreads) w[n] = n <= l ? expf(lp[n] - mx) * inv : 0.f;
   }
 }
 
-// grid: rows, block kDetThreads, dynamic LDS N floats.  G overwrites X.
+// grid: rows, block kDetThreads.  G overwrites X.
 __global__ __launch_bounds__(kDetThreads) void det_grad_kernel(float* __restrict__ XG, int64_t ldx,
                                                                const float* __restrict__ W, const float* __restrict__ dW,
                                                                int64_t ldw, int N, int T, int causal) {
-  extern __shared__ float A[];
+  __shared__ float top[2][kDetThreads];
   __shared__ float red[kDetThreads / 64];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
   const float* w = W + r * ldw;
   const float* dw = dW + r * ldw;
   float* xg = XG + r * ldx;
+  const int tb = min(T, kDetTop), c = T - tb, C = 1 << c;
+  const int cl = min(c, 4), nchunk = C >> cl;
   float delta = 0.f;
   if (causal) {
     float s = 0.f;
     for (int n = tid; n < N; n += kDetThreads) s += w[n] * dw[n];
     delta = block_sum(s, red);
   }
-  for (int n = tid; n < N; n += kDetThreads) A[n] = w[n] * (dw[n] - delta);
+  // node gradient from the two children's summed dlogw; returns the parent's sum
+  auto node = [&](int nidx, float al, float ar) {
+    const float xv = xg[nidx];
+    const float sg = 1.f / (1.f + expf(-xv));
+    xg[nidx] = (1.f - sg) * al - sg * ar;
+    return al + ar;
+  };
+  float total = 0.f;
+  if (tid < (1 << tb)) {
+    float ct[kDetChunks];
+#pragma unroll
+    for (int j = 0; j < kDetChunks; ++j) {
+      if (j < nchunk) {
+        const int base = tid * C + (j << cl);
+        const int m = 1 << cl;
+        float a[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < m) a[i] = w[base + i] * (dw[base + i] - delta);
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+          if (e < cl) {
+            const int n0 = path_node(T - cl + e, base, T);
+#pragma unroll
+            for (int i = 0; i < (1 << e); ++i) a[i] = node(n0 + i, a[2 * i], a[2 * i + 1]);
+          }
+        }
+        ct[j] = a[0];
+      }
+    }
+    // chunk roots (depth T - cl) -> subtree root (depth tb): at most three levels
+#pragma unroll
+    for (int e = 2; e >= 0; --e) {
+      if (e < c - cl) {
+        const int n0 = path_node(tb + e, tid * C, T);
+#pragma unroll
+        for (int i = 0; i < (1 << e); ++i) ct[i] = node(n0 + i, ct[2 * i], ct[2 * i + 1]);
+      }
+    }
+    total = ct[0];
+  }
+  int cur = 0;
+  top[0][tid] = total;
   __syncthreads();
-  for (int d = T - 1; d >= 0; --d) {
+  for (int d = tb - 1; d >= 0; --d) {
     const int nd = 1 << d;
-    float al[kDetPer], ar[kDetPer], xs[kDetPer];
-#pragma unroll
-    for (int j = 0; j < kDetPer; ++j) {
-      const int i = tid + kDetThreads * j;
-      if (i < nd) {
-        al[j] = A[2 * i];
-        ar[j] = A[2 * i + 1];
-        xs[j] = xg[nd - 1 + i];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kDetPer; ++j) {
-      const int i = tid + kDetThreads * j;
-      if (i < nd) {
-        const float s = 1.f / (1.f + expf(-xs[j]));
-        xg[nd - 1 + i] = (1.f - s) * al[j] - s * ar[j];
-        A[i] = al[j] + ar[j];
-      }
-    }
+    if (tid < nd) top[cur ^ 1][tid] = node(nd - 1 + tid, top[cur][2 * tid], top[cur][2 * tid + 1]);
+    cur ^= 1;
     __syncthreads();
   }
 }
@@ -210,7 +281,7 @@ __global__ __launch_bounds__(256) void haar_keys_adjoint_kernel(const float* __r
 
 hipError_t launch_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw, int64_t rows, int L, int N, int T,
                               int causal, hipStream_t st) {
-  const int smem = N * 4;
+  const int smem = causal ? N * 4 : 0;
   hipError_t e = hipFuncSetAttribute((const void*)det_weights_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(det_weights_kernel, dim3((unsigned)rows), dim3(kDetThreads), smem, st, X, ldx, W, ldw, L, N, T,
@@ -220,10 +291,7 @@ hipError_t launch_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw
 
 hipError_t launch_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows, int N,
                            int T, int causal, hipStream_t st) {
-  const int smem = N * 4;
-  hipError_t e = hipFuncSetAttribute((const void*)det_grad_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(det_grad_kernel, dim3((unsigned)rows), dim3(kDetThreads), smem, st, XG, ldx, W, dW, ldw, N, T,
+  hipLaunchKernelGGL(det_grad_kernel, dim3((unsigned)rows), dim3(kDetThreads), 0, st, XG, ldx, W, dW, ldw, N, T,
                      causal);
   return hipGetLastError();
 }

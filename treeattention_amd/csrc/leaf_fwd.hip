@@ -142,13 +142,14 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
 
 // 16-bit inputs.  One workgroup (four waves) per piece of at most kPieceFwd
 // pairs of one leaf block (bucket.hip), so the heavy low blocks of causal runs
-// are spread over many workgroups.  Every wave keeps the block's K rows (the
-// A operand of S^T = K Q^T) and V^T (the A operand of O^T = V^T P^T) in
-// registers for the whole piece; V^T is read from a row-major LDS copy with
-// transposing reads whose head-dim order puts eight consecutive dims of a
-// pair's output in one lane, so each output row leaves in 16-byte stores.
-// The piece's pair list sits in LDS and every wave loads the query rows of
-// its next two 16-pair tiles while the current one computes.
+// are spread over many workgroups.  The block's K rows (the A operand of
+// S^T = K Q^T) stay in LDS, read with 16-byte loads per tile; every wave keeps
+// V^T (the A operand of O^T = V^T P^T) in registers for the whole piece, read
+// once from a row-major LDS copy with transposing reads whose head-dim order
+// puts eight consecutive dims of a pair's output in one lane, so each output
+// row leaves in 16-byte stores.  The piece's pair list sits in LDS and every
+// wave loads the query rows of its next two 16-pair tiles while the current
+// one computes.
 template <typename E, int D, int LBP>
 __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
   using M = Mfma<E>;
@@ -157,12 +158,11 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
   constexpr int MT = LBP / 16;      // key tiles of S^T
   constexpr int KK = LBP / M::K;    // k-steps of O^T over keys
   constexpr int NP = D / 32;        // 32-dim output groups (two O^T tiles each)
-  constexpr bool kKreg = LBP * D <= 64 * 128;
   constexpr int VS = D + 16;        // padded LDS row stride (elements)
   extern __shared__ __align__(16) char smem[];
   int* ord_s = (int*)smem;                  // [kPieceFwd] (l << 6) | u
   E* Vs = (E*)(smem + kPieceFwd * 4);       // [LBP][VS]
-  E* Ks = Vs + LBP * VS;                    // [LBP][VS] (K in LDS when it does not fit in registers)
+  E* Ks = Vs + LBP * VS;                    // [LBP][VS]
 
   int bh, piece;
   if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.npiece, bh, piece)) return;
@@ -190,21 +190,10 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
     if (key < LB) {
       const int64_t tok = (int64_t)beta * LB + key;
       vv = *(const uint4*)(v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
-      if (!kKreg && k) kv = *(const uint4*)(k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
+      if (k) kv = *(const uint4*)(k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
     }
     *(uint4*)(Vs + key * VS + c) = vv;
-    if constexpr (!kKreg) *(uint4*)(Ks + key * VS + c) = kv;
-  }
-  // K rows straight from global memory into A fragments (zero past LB)
-  F kf[kKreg ? MT : 1][KS];
-  if constexpr (kKreg) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int key = 16 * mt + col;
-      const E* kr = (k && key < LB) ? k + bb * a.ksb + ((int64_t)beta * LB + key) * a.ksl + h * a.ksh : nullptr;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = kr ? ld_frag(kr + ks * M::K + M::KPL * g) : zero_frag<E>();
-    }
+    *(uint4*)(Ks + key * VS + c) = kv;
   }
   __syncthreads();
   // V^T fragments (dims x keys), dims permuted so each lane's outputs are
@@ -236,10 +225,8 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
     for (int mt = 0; mt < MT; ++mt) {
       sacc[mt] = zero4();
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if constexpr (kKreg) sacc[mt] = M::mma(kf[mt][ks], cur.f[ks], sacc[mt]);
-        else sacc[mt] = M::mma(ld_frag(Ks + (16 * mt + col) * VS + ks * M::K + M::KPL * g), cur.f[ks], sacc[mt]);
-      }
+      for (int ks = 0; ks < KS; ++ks)
+        sacc[mt] = M::mma(ld_frag(Ks + (16 * mt + col) * VS + ks * M::K + M::KPL * g), cur.f[ks], sacc[mt]);
     }
     const int kmax = valid ? (a.causal ? min(LB, l + coff + 1) : LB) : 0;
     float mx = -__builtin_inff();
@@ -340,7 +327,7 @@ static int fwd_smem_t() {
 }
 
 static int fwd16_smem(int D, int LBP) {
-  return kPieceFwd * 4 + (LBP * D <= 64 * 128 ? 1 : 2) * LBP * (D + 16) * 2;
+  return kPieceFwd * 4 + 2 * LBP * (D + 16) * 2;
 }
 
 int leaf_fwd_smem(const Plan& P) {
