@@ -260,6 +260,23 @@ struct BwdTrTile {
 };
 
 
+// One pair column's operands for a tile: query and output-gradient row
+// fragments, the pair's summed sample weight, its query row (-1: padding) and
+// its (b, l, h, u) slot.
+template <typename E, int D>
+struct PairRows {
+  RowFrags<E, D> q, g;
+  float w;
+  int l;
+  int64_t sl;
+  // Waits here for the loads of this set; no memory operation moves above.
+  __device__ __forceinline__ void pin() const {
+#pragma unroll
+    for (int ks = 0; ks < D / Mfma<E>::K; ++ks) asm volatile("" ::"v"(q.f[ks]), "v"(g.f[ks]) : "memory");
+    asm volatile("" ::"v"(w) : "memory");
+  }
+};
+
 // An MFMA operand fragment of k = 8 values: rows k0a..k0a+3 then k0b..k0b+3.
 template <typename E>
 __device__ __forceinline__ typename Mfma<E>::frag tr_frag(const E* X, int rs, int k0a, int k0b, int n0, int lane) {
@@ -298,49 +315,68 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
   const E* v = (const E*)a.v;
   const E* go = (const E*)a.g;
 
-  for (int e = tid; e < LBP * D / 8; e += NW * 64) {
-    const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
-    const int64_t tok = (int64_t)beta * LB + key;
-    if (key < LB && k) mov8(Ks + key * RS + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
-    else zero8e(Ks + key * RS + c);
-    if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
-    else zero8e(Vs + key * RS + c);
+  {  // stage the block's K and V rows: every load issued before the first LDS write
+    constexpr int NST = (LBP * D / 8 + NW * 64 - 1) / (NW * 64);
+    uint4 kr[NST], vr[NST];
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int e = tid + i * NW * 64;
+      const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+      const int64_t tok = (int64_t)beta * LB + key;
+      const bool in = e < LBP * D / 8 && key < LB;
+      kr[i] = in && k ? *(const uint4*)(k + bb * a.ksb + tok * a.ksl + h * a.ksh + c) : make_uint4(0, 0, 0, 0);
+      vr[i] = in ? *(const uint4*)(v + bb * a.vsb + tok * a.vsl + h * a.vsh + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int e = tid + i * NW * 64;
+      const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
+      if (e < LBP * D / 8) {
+        *(uint4*)(Ks + key * RS + c) = kr[i];
+        *(uint4*)(Vs + key * RS + c) = vr[i];
+      }
+    }
   }
   __syncthreads();
 
-  // phase B output tiles of this wave: keys 16 mk0 .. +31, dims 16 nd0 .. +31
-  constexpr int MKW = LBP / 32;                     // key-tile pairs
-  constexpr int NDW = D / 32;                       // dim-tile pairs
-  constexpr int NBLK = MKW * NDW;                   // 2x2 blocks per output
-  constexpr int NB = (NBLK + NW - 1) / NW;          // blocks per wave
-  f32x4 dvacc[NB][4], dkacc[NB][4];
+  // phase B: waves 0-3 accumulate dV = (wP)^T dout, waves 4-7 dK = dz^T Q;
+  // wave w & 3 owns the quarter (key half (w & 3) >> 1, dim half w & 1):
+  // MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand reads per MK2 * ND2 MFMAs
+  constexpr int MK2 = LBP / 32, ND2 = D / 32;
+  const bool dkw = w >= 4;
+  const int mkb = MK2 * ((w & 3) >> 1), ndb = ND2 * (w & 1);
+  const E* Ab = dkw ? Zs : Ps;
+  const E* Bb = dkw ? Qs : Gs;
+  f32x4 acc[MK2][ND2];
 #pragma unroll
-  for (int i = 0; i < NB; ++i)
+  for (int x = 0; x < MK2; ++x)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) { dvacc[i][t] = zero4(); dkacc[i][t] = zero4(); }
+    for (int y = 0; y < ND2; ++y) acc[x][y] = zero4();
 
+  // Software pipeline over 128-pair tiles with two register sets: a tile
+  // first waits for its own set (loaded one tile earlier), then issues the
+  // loads of the next tile into the other set and reads the pair index of the
+  // tile after.  The wait sits before the new loads on purpose: vmcnt counts
+  // loads and stores alike, so any wait placed after them would also wait for
+  // them.  The loop is unrolled twice so the sets never move between registers.
   const int* ord = a.order + (int64_t)bh * LS;
   const int pcol = 16 * w + col;  // this lane's pair column within the tile
-  int ent = start + pcol < end ? ord[start + pcol] : -1;
-  RowFrags<E, D> qf, gf;
-  {
-    const int64_t lo = ent >= 0 ? (int64_t)(ent / S) : 0;
-    qf.load(ent >= 0 ? q + bb * a.qsb + lo * a.qsl + h * a.qsh : nullptr, g);
-    gf.load(ent >= 0 ? go + bb * a.gsb + lo * a.gsl + h * a.gsh : nullptr, g);
-  }
-  for (int t0 = start; t0 < end; t0 += QT) {
-    const int cur = ent;
-    const RowFrags<E, D> qc = qf, gc = gf;
-    {
-      const int t1 = t0 + QT;
-      ent = t1 + pcol < end ? ord[t1 + pcol] : -1;
-      const int64_t lo = ent >= 0 ? (int64_t)(ent / S) : 0;
-      qf.load(ent >= 0 ? q + bb * a.qsb + lo * a.qsl + h * a.qsh : nullptr, g);
-      gf.load(ent >= 0 ? go + bb * a.gsb + lo * a.gsl + h * a.gsh : nullptr, g);
-    }
-    const bool valid = cur >= 0;
-    const int l = valid ? cur / S : 0, u = valid ? cur - l * S : 0;
-    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+  auto idx = [&](int t) { return t + pcol < end ? ord[t + pcol] : -1; };
+  auto fetch = [&](int e, PairRows<E, D>& r) {  // pair entry e = l * S + u, or -1
+    const int l = e >= 0 ? e / S : 0;
+    r.l = e >= 0 ? l : -1;
+    r.sl = (((int64_t)bb * a.L + l) * a.H + h) * S + (e >= 0 ? e - l * S : 0);
+    r.q.load(e >= 0 ? q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh : nullptr, g);
+    r.g.load(e >= 0 ? go + bb * a.gsb + (int64_t)l * a.gsl + h * a.gsh : nullptr, g);
+    r.w = e >= 0 ? a.slot_weight[r.sl] : 0.f;
+  };
+  auto tile = [&](const PairRows<E, D>& c) {
+    const bool valid = c.l >= 0;
+    const int l = valid ? c.l : 0;
+    const int64_t sl = c.sl;
+    const float wt = c.w;
+    const RowFrags<E, D>& qc = c.q;
+    const RowFrags<E, D>& gc = c.g;
 
     // ---- phase A: this wave's 16 pairs
     f32x4 sacc[LBP / 16], pacc[LBP / 16];
@@ -394,18 +430,17 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
         delta += sacc[mt][r] * pacc[mt][r];
       }
     delta = col_sum(delta);
-    const float wt = valid ? a.slot_weight[qh * S + u] : 0.f;
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) pacc[mt][r] = wt * sacc[mt][r] * (pacc[mt][r] - delta);
-    if (valid && g == 0) a.delta[qh * S + u] = delta;
+    if (valid && g == 0) a.delta[sl] = delta;
 
     // dq_pair^T = K^T dz^T: K^T fragments read transposed from Ks in the
     // accumulator's key order (keys 32ks + 4g.. and 32ks + 16 + 4g..)
     // K^T fragments with permuted head dims: each lane ends with eight
     // consecutive dims of its pair's dq row, one 16-byte store per 32 dims
-    E* dqp = (E*)a.dq_part + (qh * S + u) * D + 8 * g;
+    E* dqp = (E*)a.dq_part + sl * D + 8 * g;
 #pragma unroll
     for (int p = 0; p < D / 32; ++p) {
       f32x4 o0 = zero4(), o1 = zero4();
@@ -451,56 +486,53 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
     }
     __syncthreads();
 
-    // ---- phase B: dV, dK over the tile's 128 pairs, 2x2 output tiles per wave
+    // ---- phase B: this wave's quarter of dV or dK over the tile's 128 pairs
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int blk = w + NW * i;
-      if (blk < NBLK) {
-        const int mk0 = 2 * (blk / NDW), nd0 = 2 * (blk % NDW);
+    for (int ks = 0; ks < QT / M::K; ++ks) {
+      const int ka = 32 * ks + 8 * g, kb = ka + 4;
+      typename M::frag af[MK2], bf[ND2];
 #pragma unroll
-        for (int ks = 0; ks < QT / M::K; ++ks) {
-          const int ka = 32 * ks + 8 * g, kb = ka + 4;
-          typename M::frag pa[2], za[2], gb[2], qb[2];
+      for (int x = 0; x < MK2; ++x) af[x] = tr_frag(Ab, PS, ka, kb, 16 * (mkb + x), lane);
 #pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            pa[x] = tr_frag(Ps, PS, ka, kb, 16 * (mk0 + x), lane);
-            za[x] = tr_frag(Zs, PS, ka, kb, 16 * (mk0 + x), lane);
-            gb[x] = tr_frag(Gs, RS, ka, kb, 16 * (nd0 + x), lane);
-            qb[x] = tr_frag(Qs, RS, ka, kb, 16 * (nd0 + x), lane);
-          }
+      for (int y = 0; y < ND2; ++y) bf[y] = tr_frag(Bb, RS, ka, kb, 16 * (ndb + y), lane);
 #pragma unroll
-          for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < MK2; ++x)
 #pragma unroll
-            for (int y = 0; y < 2; ++y) {
-              dvacc[i][2 * x + y] = M::mma(pa[x], gb[y], dvacc[i][2 * x + y]);
-              dkacc[i][2 * x + y] = M::mma(za[x], qb[y], dkacc[i][2 * x + y]);
-            }
-        }
-      }
+        for (int y = 0; y < ND2; ++y) acc[x][y] = M::mma(af[x], bf[y], acc[x][y]);
     }
+  };
+
+  PairRows<E, D> ra, rb;
+  int e1 = idx(start + QT);
+  fetch(idx(start), ra);
+  for (int t0 = start; t0 < end; t0 += 2 * QT) {
+    ra.pin();
+    const int e2 = idx(t0 + 2 * QT);
+    fetch(e1, rb);
+    tile(ra);
+    if (t0 + QT >= end) break;
+    rb.pin();
+    e1 = idx(t0 + 3 * QT);
+    fetch(e2, ra);
+    tile(rb);
   }
 
   E* dv = (E*)a.dv;
+  if (dkw && !a.dk_leaf) return;
 #pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    const int blk = w + NW * i;
-    if (blk >= NBLK) continue;
-    const int mk0 = 2 * (blk / NDW), nd0 = 2 * (blk % NDW);
+  for (int x = 0; x < MK2; ++x)
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int y = 0; y < ND2; ++y)
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = 16 * (mk0 + x) + 4 * g + r;
-          if (key < LB) {
-            const int64_t tok = (int64_t)beta * LB + key;
-            const int d = 16 * (nd0 + y) + col;
-            dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[i][2 * x + y][r];
-            if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[i][2 * x + y][r] * a.scale;
-          }
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * (mkb + x) + 4 * g + r;
+        if (key < LB) {
+          const int64_t tok = (int64_t)beta * LB + key;
+          const int d = 16 * (ndb + y) + col;
+          if (dkw) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = acc[x][y][r] * a.scale;
+          else dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)acc[x][y][r];
         }
-  }
+      }
 }
 
 template <typename E, int D, int LBP>

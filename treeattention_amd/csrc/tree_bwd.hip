@@ -225,12 +225,13 @@ __device__ __forceinline__ int grp_down1(int x) {
 // for the node's children without sampled blocks.  Every entry has one
 // writer and every sum a fixed order: deterministic, no atomics.  Clamped
 // logits get 0.
-template <typename E, int P>
+// kB: the branching factor when known at compile time (2 or 4), else 0.
+template <typename E, int P, int kB>
 __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols, int S, int nq, float maxhalf,
                                           const float* Xs, const int* lf, const float* dls, const int* cn, E* Gm,
                                           int tid) {
   constexpr int LP = P <= 1 ? 0 : P <= 2 ? 1 : P <= 4 ? 2 : P <= 8 ? 3 : P <= 16 ? 4 : P <= 32 ? 5 : 6;
-  const int b = G.b, lb = G.lb;
+  const int b = kB > 0 ? kB : G.b, lb = kB == 2 ? 1 : kB == 4 ? 2 : G.lb;
   const int sh = lb * (G.T - d), sh2 = sh - lb;
   const int lane = tid & 63;
   for (int e0 = 0; e0 < (kQueryTile << LP); e0 += 256) {
@@ -258,7 +259,7 @@ __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols
         const int kc = grp_up<P, O>(crow);
         const int kn = grp_up<P, O>(node);
         const int h0 = grp_up<P, O>(has0);
-        const int h1 = grp_up<P, O>(has1);
+        const int h1 = kB > 0 ? 0 : grp_up<P, O>(has1);  // b <= 32: has1 stays 0
         if (u >= O) {
           if (kc == crow) vc += tc;
           if (kn == node) {
@@ -286,24 +287,53 @@ __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols
     const int base = (node << lb) - c0;
     if ((cend || nend) && base >= 0 && base < ncols) {
       const float* xr = Xs + qi * kXS + base;
-      float mx = -__builtin_inff();
-      for (int j = 0; j < b; ++j) mx = fmaxf(mx, clamp_h(xr[j], maxhalf));
-      float se = 0.f;
-      for (int j = 0; j < b; ++j) se += __expf(clamp_h(xr[j], maxhalf) - mx);
-      const float lse = mx + __logf(se);
       E* gr = Gm + qi * kGS + base;
-      if (cend) {
-        const int j = crow & (b - 1);
-        const float x = xr[j];
-        const bool live = x >= -maxhalf && x <= maxhalf;
-        gr[j] = (E)(live ? vc - __expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
-      }
-      if (nend) {
-        for (int j = 0; j < b; ++j) {
-          if (j < 32 ? ((has0 >> j) & 1) : ((has1 >> (j - 32)) & 1)) continue;
+      if constexpr (kB > 0) {
+        // the node's kB logits in one LDS read (base is a multiple of kB)
+        float xv[kB], ev[kB];
+        if constexpr (kB == 4) {
+          const float4 t = *(const float4*)xr;
+          xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
+        } else {
+          const float2 t = *(const float2*)xr;
+          xv[0] = t.x; xv[1] = t.y;
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < kB; ++j) mx = fmaxf(mx, clamp_h(xv[j], maxhalf));
+        float se = 0.f;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          ev[j] = __expf(clamp_h(xv[j], maxhalf) - mx);
+          se += ev[j];
+        }
+        const float pa = An / se;  // p_j A_n = ev[j] * pa
+        const int jc = crow & (kB - 1);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const bool live = xv[j] >= -maxhalf && xv[j] <= maxhalf;
+          if (cend && j == jc) gr[j] = (E)(live ? vc - ev[j] * pa : 0.f);
+          else if (nend && !((has0 >> j) & 1)) gr[j] = (E)(live ? -ev[j] * pa : 0.f);
+        }
+      } else {
+        float mx = -__builtin_inff();
+        for (int j = 0; j < b; ++j) mx = fmaxf(mx, clamp_h(xr[j], maxhalf));
+        float se = 0.f;
+        for (int j = 0; j < b; ++j) se += __expf(clamp_h(xr[j], maxhalf) - mx);
+        const float lse = mx + __logf(se);
+        if (cend) {
+          const int j = crow & (b - 1);
           const float x = xr[j];
           const bool live = x >= -maxhalf && x <= maxhalf;
-          gr[j] = (E)(live ? -__expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
+          gr[j] = (E)(live ? vc - __expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
+        }
+        if (nend) {
+          for (int j = 0; j < b; ++j) {
+            if (j < 32 ? ((has0 >> j) & 1) : ((has1 >> (j - 32)) & 1)) continue;
+            const float x = xr[j];
+            const bool live = x >= -maxhalf && x <= maxhalf;
+            gr[j] = (E)(live ? -__expf(clamp_h(x, maxhalf) - lse) * An : 0.f);
+          }
         }
       }
     }
@@ -318,7 +348,8 @@ __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols
 // and G^T goes to global for the summary-gradient product.  The epilogue adds
 // the leaf parts dq_pair of each query's distinct blocks.
 // kP: lanes per query in build_g (16: S <= 16, DPP scans; 64: shuffles).
-template <typename E, int D, int kP>
+// kB: the branching factor when known at compile time (2 or 4), else 0.
+template <typename E, int D, int kP, int kB>
 __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   using M = Mfma<E>;
   using F = typename M::frag;
@@ -450,7 +481,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       z8(sm.Gm + r * kGS + cc);
     }
     __syncthreads();
-    build_g_p<E, kP>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    build_g_p<E, kP, kB>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
     __syncthreads();
     if (a.refc) {
       // boundary-mass gradient of the reference causal mode (ref_causal_grad_kernel)
@@ -779,17 +810,18 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
   const int smem_q = tree_smem(P);
   const unsigned qtiles = (unsigned)(P.Lp / kQueryTile);
-  if (P.S <= 16) {
-    hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D, 16>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
+  auto launch_dq = [&](auto kern) -> hipError_t {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((tree_dq_kernel<E, D, 16>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
-  } else {
-    hipError_t e = hipFuncSetAttribute((const void*)tree_dq_kernel<E, D, 64>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem_q);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((tree_dq_kernel<E, D, 64>), dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
-  }
+    hipLaunchKernelGGL(kern, dim3(qtiles, P.BH), dim3(256), smem_q, st, a);
+    return hipSuccess;
+  };
+  hipError_t e = hipSuccess;
+  if (P.S > 16) e = launch_dq(tree_dq_kernel<E, D, 64, 0>);
+  else if (P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 16, 4>);
+  else if (P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 16, 2>);
+  else e = launch_dq(tree_dq_kernel<E, D, 16, 0>);
+  if (e != hipSuccess) return e;
   if (P.geo.T > 0) {
     const unsigned chunks = (unsigned)((P.geo.NS / 16 + 8 * kDcRows - 1) / (8 * kDcRows));
     hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(chunks, P.qsplit, P.BH), dim3(512), 0, st, a);
