@@ -31,6 +31,7 @@ struct BucketArgs {
 template <bool kScatter>
 __global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) {
   __shared__ uint32_t bits[kWin * kWords];
+  __shared__ int hb[kScatter ? kWin : 1];  // scatter: the window's run bases of this chunk
   const int c = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
   const int tid = threadIdx.x;
   const int l = c * kQueryChunk + tid;
@@ -41,14 +42,27 @@ __global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) 
   const int64_t LS = (int64_t)a.L * a.S;
   const uint32_t bit = 1u << (tid & 31);
   const int word = tid >> 5;
+  // fn(u, leaf) for this query's slots, eight slot loads in flight at a time
+  auto for_slots = [&](auto fn) {
+    for (int u0 = 0; u0 < n; u0 += 8) {
+      int lv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lv[j] = u0 + j < n ? mine[u0 + j] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (u0 + j < n) fn(u0 + j, lv[j]);
+    }
+  };
   for (int w0 = 0; w0 < a.NL; w0 += kWin) {
     const int wn = min(kWin, a.NL - w0);
     for (int i = tid; i < wn * kWords; i += kQueryChunk) bits[i] = 0u;
+    if constexpr (kScatter)
+      for (int beta = tid; beta < wn; beta += kQueryChunk) hb[beta] = a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c];
     __syncthreads();
-    for (int u = 0; u < n; ++u) {
-      const int beta = mine[u] - w0;
+    for_slots([&](int u, int leaf) {
+      const int beta = leaf - w0;
       if (beta >= 0 && beta < wn) atomicOr(&bits[beta * kWords + word], bit);
-    }
+    });
     __syncthreads();
     if constexpr (!kScatter) {
       for (int beta = tid; beta < wn; beta += kQueryChunk) {
@@ -58,15 +72,14 @@ __global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) 
         a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c] = cnt;
       }
     } else {
-      for (int u = 0; u < n; ++u) {
-        const int beta = mine[u] - w0;
-        if (beta < 0 || beta >= wn) continue;
+      for_slots([&](int u, int leaf) {
+        const int beta = leaf - w0;
+        if (beta < 0 || beta >= wn) return;
         const uint32_t* bm = bits + beta * kWords;
         int r = __popc(bm[word] & (bit - 1u));
         for (int k = 0; k < word; ++k) r += __popc(bm[k]);
-        const int base = a.hist[((int64_t)bh * a.NL + w0 + beta) * a.nchunk + c];
-        a.order[(int64_t)bh * LS + base + r] = l * a.S + u;
-      }
+        a.order[(int64_t)bh * LS + hb[beta] + r] = l * a.S + u;
+      });
     }
     __syncthreads();
   }
