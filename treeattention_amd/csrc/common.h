@@ -212,7 +212,17 @@ struct RowFrags {
     for (int ks = 0; ks < D / Mfma<E>::K; ++ks)
       f[ks] = row ? ld_frag(row + ks * Mfma<E>::K + Mfma<E>::KPL * g) : zero_frag<E>();
   }
+  // The compiler waits here for the loads of these fragments, and no memory
+  // operation moves above this point.  A software pipeline calls it before
+  // issuing the next tile's loads: vmcnt counts loads and stores alike, so a
+  // wait placed after newer loads (with stores in between) waits for all of
+  // them.
+  __device__ __forceinline__ void pin() const {
+#pragma unroll
+    for (int ks = 0; ks < D / Mfma<E>::K; ++ks) asm volatile("" ::"v"(f[ks]) : "memory");
+  }
 };
+__device__ __forceinline__ void pin_value(float x) { asm volatile("" ::"v"(x) : "memory"); }
 
 // X[16w + i][c] = A_i . B_row(c) for columns c < ncols (row row0 + c of the
 // row-major B matrix with row length D; tile columns past ncols read row

@@ -271,9 +271,9 @@ struct PairRows {
   int64_t sl;
   // Waits here for the loads of this set; no memory operation moves above.
   __device__ __forceinline__ void pin() const {
-#pragma unroll
-    for (int ks = 0; ks < D / Mfma<E>::K; ++ks) asm volatile("" ::"v"(q.f[ks]), "v"(g.f[ks]) : "memory");
-    asm volatile("" ::"v"(w) : "memory");
+    q.pin();
+    g.pin();
+    pin_value(w);
   }
 };
 

@@ -206,20 +206,34 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
 
   const int ntile = (np + 15) >> 4;
   const int coff = a.coff - beta * LB;  // key j of the block is visible to query l iff j <= l + coff
-  auto qrow = [&](int t) -> const E* {
-    const int i = 16 * t + col;
-    if (t >= ntile || i >= np) return nullptr;
-    return q + bb * a.qsb + (int64_t)(ord_s[i] >> 6) * a.qsl + h * a.qsh;
+  // Three-set ring of (query-row fragments, summed sample weight): a step
+  // waits for its own set (loaded two steps earlier), then issues the loads
+  // of the tile two steps ahead, so no wait in a step covers a load issued
+  // in the same step.
+  struct QSet {
+    RowFrags<E, D> q;
+    float w;
   };
-  RowFrags<E, D> qb[3];
-  qb[0].load(qrow(w), g);
-  qb[1].load(qrow(w + 4), g);
-  auto step = [&](int t, RowFrags<E, D>& cur, RowFrags<E, D>& nxt) {
+  auto fetch = [&](int t, QSet& r) {
+    const int i = 16 * t + col;
+    const bool ok = t < ntile && i < np;
+    const int ent = ok ? ord_s[i] : 0;
+    const int l = ent >> 6, u = ent & 63;
+    r.q.load(ok ? q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh : nullptr, g);
+    r.w = ok ? a.slot_weight[(((int64_t)bb * a.L + l) * a.H + h) * S + u] : 0.f;
+  };
+  QSet qb[3];
+  fetch(w, qb[0]);
+  fetch(w + 4, qb[1]);
+  auto step = [&](int t, QSet& cs, QSet& nxt) {
+    cs.q.pin();
+    pin_value(cs.w);
+    const RowFrags<E, D>& cur = cs.q;
     const int i = 16 * t + col;
     const bool valid = i < np;
     const int ent = valid ? ord_s[i] : 0;
     const int l = ent >> 6, u = ent & 63;
-    nxt.load(qrow(t + 8), g);
+    fetch(t + 8, nxt);
     f32x4 sacc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -255,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
       }
     sum = col_sum(sum);
     const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    const float f = (valid && sum > 0.f) ? a.slot_weight[qh * S + u] * __builtin_amdgcn_rcpf(sum) : 0.f;
+    const float f = (valid && sum > 0.f) ? cs.w * __builtin_amdgcn_rcpf(sum) : 0.f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sacc[mt] *= f;
     F pf[KK];
