@@ -147,6 +147,37 @@ int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
                const float* uniforms, uint64_t seed, void* out, float* weights,
                void* record, void* workspace, void* stream);
 
+/* Packed path record of the reference (_autograd.py:68-90,179-216), the
+ * stable on-device format of the sampled paths: per (position, batch, head,
+ * sample) the root-to-leaf directions as a bit string, bit p (p = 0 at the
+ * root) in byte p/8 at bit p%8, ta_path_bytes = ceil(log2(NL)/8) bytes,
+ * layout (L, B, H, S, bytes) contiguous.  In a b-ary tree each level's child
+ * digit takes log2(b) bits, high bit first, so the bit string is the leaf
+ * block id most-significant bit first; for the reference's binary tree bit d
+ * is the direction at depth d (heap walk node <- 2 node + 1 + dir).
+ * `num_leaf_blocks` (NL) is a power of two; leaf ids are int32 in [0, NL)
+ * with (batch, position, head, sample) element strides `leaf_strides[4]`
+ * (the record's TA_REC_LEAVES array is (B, L, H, S) contiguous). */
+int ta_path_bytes(int64_t num_leaf_blocks, int64_t* bytes);
+int ta_pack_paths(const int32_t* leaf, const int64_t* leaf_strides, int64_t B, int64_t L, int64_t H,
+                  int64_t S, int64_t num_leaf_blocks, uint8_t* packed, void* stream);
+int ta_unpack_paths(const uint8_t* packed, int64_t B, int64_t L, int64_t H, int64_t S,
+                    int64_t num_leaf_blocks, int32_t* leaf, const int64_t* leaf_strides, void* stream);
+
+/* Path replay: ta_sample with every decision taken from `packed` (the layout
+ * above, NL = N / leaf_block) instead of the Gumbel-max draw; log-probs,
+ * weights and the record follow as in sampling, so replaying a forward's own
+ * paths reproduces it bit for bit.  Non-causal problems only, like the
+ * reference's replay.  Replaces _replay_non_causal_paths (_autograd.py:261-350)
+ * and replay_non_causal_paths_forward (treeattn_cuda.cpp:142). */
+int ta_replay(const ta_problem* p, const void* q, const uint8_t* packed, float* weights,
+              void* record, void* stream);
+
+/* Whole forward with replayed paths: ta_pool + ta_replay + ta_bucket + ta_leaf_forward. */
+int ta_forward_replay(const ta_problem* p, const void* q, const void* k, const void* v,
+                      const uint8_t* packed, void* out, float* weights, void* record,
+                      void* workspace, void* stream);
+
 /* Backward, leaf-block part: dv (complete), the leaf contribution to dk and
  * per-pair dq and dout.o into `workspace`.  Replaces
  * scatter_weighted_grad_v_forward (treeattn_cuda.cpp:290) and the value side

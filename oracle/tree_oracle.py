@@ -36,6 +36,11 @@ Parity status per function (what pins it, all in ``tests/test_oracle.py``):
   textbook masked softmax attention.
 * ``tree_backward``: torch autograd through an independent torch restatement
   and central finite differences.
+* ``pack_paths`` / ``unpack_paths``: the heap walk of the reference
+  (``heap_walk``, ``_autograd.py:219,312-315``) on random directions, packed
+  depth by depth as the reference does (``_autograd.py:214-216``), and round
+  trips; the golden fixtures' sampled indices replayed on the GPU reproduce
+  the reference's outputs (``tests/test_gpu_paths.py``).
 * Causal mode of the reference (``_tree_mha.py:125-268,379-394``) is NOT
   restated here: the generalized causal semantics below sample exactly from
   the tree distribution restricted to allowed leaves, which the reference's
@@ -629,3 +634,50 @@ def attention_fwd_bwd(q, k, v, dout, branching, leaf_block, U, causal, tree_mode
         dk = dk_leaf + pool_adjoint(dC, k.shape[1], branching, leaf_block, tree_mode)
         res.update(dq=dq, dk=dk, dv=dv, dC=dC)
     return res
+
+
+# --------------------------------------------------------------------------
+# Packed path record (_autograd.py:68-90,179-216).
+# --------------------------------------------------------------------------
+
+
+def path_bytes(num_leaf_blocks: int) -> int:
+    """Bytes per packed path: ``_path_bit_bytes`` (``_autograd.py:68-70``)."""
+    return (max(int(num_leaf_blocks).bit_length() - 1, 0) + 7) // 8
+
+
+def pack_paths(idx: np.ndarray, num_leaf_blocks: int) -> np.ndarray:
+    """Leaf block ids ``(..., S)`` -> packed bits ``(..., S, path_bytes)`` uint8.
+
+    Bit ``p`` of a path (``p = 0`` at the root) sits in byte ``p // 8`` at bit
+    ``p % 8`` (``_autograd.py:214-216``); the path's bits are the id's, most
+    significant first (for a binary heap, bit ``d`` is the direction taken at
+    depth ``d``; in a ``b``-ary tree each level's digit takes ``log2 b`` bits).
+    """
+    nbits = int(num_leaf_blocks).bit_length() - 1
+    idx = np.asarray(idx, dtype=np.int64)
+    out = np.zeros(idx.shape + (path_bytes(num_leaf_blocks),), dtype=np.uint8)
+    for p in range(nbits):
+        bit = (idx >> (nbits - 1 - p)) & 1
+        out[..., p // 8] |= (bit << (p % 8)).astype(np.uint8)
+    return out
+
+
+def unpack_paths(packed: np.ndarray, num_leaf_blocks: int) -> np.ndarray:
+    """Inverse of ``pack_paths``: ``(..., bytes)`` uint8 -> leaf block ids (int64)."""
+    nbits = int(num_leaf_blocks).bit_length() - 1
+    packed = np.asarray(packed, dtype=np.int64)
+    idx = np.zeros(packed.shape[:-1], dtype=np.int64)
+    for p in range(nbits):
+        idx |= ((packed[..., p // 8] >> (p % 8)) & 1) << (nbits - 1 - p)
+    return idx
+
+
+def heap_walk(directions: np.ndarray) -> np.ndarray:
+    """The reference's root-to-leaf walk: per depth ``node <- 2 node + 1 + dir``,
+    leaf ``= node - K`` with ``K = 2^T - 1`` (``_autograd.py:219,312-315``)."""
+    T = directions.shape[-1]
+    node = np.zeros(directions.shape[:-1], dtype=np.int64)
+    for d in range(T):
+        node = 2 * node + 1 + directions[..., d].astype(np.int64)
+    return node - (2 ** T - 1)

@@ -4,7 +4,8 @@ Entry points mirror the reference interfaces: ``hierarchical_attention``
 (treeattn-torch / treeattn-cuda op, stochastic and deterministic modes),
 ``StochasticTreeAttention`` / ``DeterministicTreeAttention`` (autograd
 Functions), ``attn_fn`` / ``adapter`` (attn-bench kernel contract), plus
-``tree_attention`` for the generalized tree (branching, leaf blocks).
+``tree_attention`` for the generalized tree (branching, leaf blocks), and
+``pack_paths`` / ``unpack_paths`` for the reference's packed path record.
 """
 
 from .api import (
@@ -21,8 +22,11 @@ from .function import (
     StochasticTreeAttention,
     TreeAttentionFunction,
     TreeOptions,
+    pack_paths,
+    path_bytes,
     tree_backward,
     tree_forward,
+    unpack_paths,
 )
 
 __all__ = [
@@ -34,9 +38,12 @@ __all__ = [
     "adapter",
     "attn_fn",
     "hierarchical_attention",
+    "pack_paths",
+    "path_bytes",
     "resolve_num_samples",
     "resolve_tree_config",
     "tree_attention",
     "tree_backward",
     "tree_forward",
+    "unpack_paths",
 ]

@@ -14,6 +14,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libtreeattn_amd.so")
 
 TA_OK = 0
+TA_ERR_INVALID, TA_ERR_UNSUPPORTED, TA_ERR_LAUNCH = 1, 2, 3
 TA_F32, TA_BF16, TA_F16 = 0, 1, 2
 TA_TREE_NATURAL, TA_TREE_COMPAT, TA_TREE_NODEKEYS = 0, 1, 2
 TA_CAUSAL_NONE, TA_CAUSAL_EXACT, TA_CAUSAL_REFERENCE = 0, 1, 2
@@ -70,6 +71,11 @@ EXPORTS = (
     "ta_det_grad",
     "ta_haar_keys",
     "ta_haar_keys_adjoint",
+    "ta_path_bytes",
+    "ta_pack_paths",
+    "ta_unpack_paths",
+    "ta_replay",
+    "ta_forward_replay",
 )
 
 _lock = threading.Lock()
@@ -117,6 +123,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_haar_keys.argtypes = [ctypes.c_int, vp, i64p, vp, i64, i64, i64, i64, vp]
     lib.ta_haar_keys_adjoint.restype = ctypes.c_int
     lib.ta_haar_keys_adjoint.argtypes = [ctypes.c_int, vp, vp, i64p, i64, i64, i64, i64, vp]
+    lib.ta_path_bytes.restype = ctypes.c_int
+    lib.ta_path_bytes.argtypes = [i64, i64p]
+    lib.ta_pack_paths.restype = ctypes.c_int
+    lib.ta_pack_paths.argtypes = [vp, i64p, i64, i64, i64, i64, i64, vp, vp]
+    lib.ta_unpack_paths.restype = ctypes.c_int
+    lib.ta_unpack_paths.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64p, vp]
+    lib.ta_replay.restype = ctypes.c_int
+    lib.ta_replay.argtypes = [P, vp, vp, vp, vp, vp]
+    lib.ta_forward_replay.restype = ctypes.c_int
+    lib.ta_forward_replay.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp]
 
 
 def load() -> ctypes.CDLL:

@@ -97,12 +97,18 @@ def hierarchical_attention(
     max_logit: float = _DEFAULT_MAX_LOGIT,
     seed: int = 0,
     uniforms: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor]:
+    paths: torch.Tensor | None = None,
+    return_paths: bool = False,
+):
     """Hierarchical attention, reference signature (``_tree_mha.py:324-413``).
 
     ``mode="stochastic"``: ``uniforms`` (optional, float32 ``(B, L, H, S, T,
     2)``, contiguous) replaces the Gumbel noise stream; without it the counter
     RNG with ``seed`` supplies it, so equal inputs give equal outputs.
+    ``paths`` (optional, non-causal): the reference's packed path record
+    ``(L, B, H, S, ceil(log2(N)/8))`` uint8 (``_autograd.py:68-90``) to replay
+    instead of sampling; ``return_paths=True`` returns ``(out, weights,
+    packed_paths)`` with the forward's own paths in that format.
     ``mode="deterministic"``: exact attention over every leaf, weights
     ``(L, B, H, N)`` (``_tree_mha.py:271-321``); ``N`` a power of two.
     """
@@ -125,11 +131,13 @@ def hierarchical_attention(
     k = key.reshape(max(K, 0), B, H, D) if K > 0 else key.new_empty((0, B, H, D))
     v = value.reshape(N, B, H, D)
     if mode == "deterministic":
+        if paths is not None or return_paths:
+            raise ValueError("paths / return_paths apply to mode='stochastic'")
         out, weights = DeterministicTreeAttention.apply(q, k, v, bool(is_causal))
         return out.reshape(L, B, E), weights
-    out, weights = StochasticTreeAttention.apply(q, k, v, num_samples, block_size, max_logit, is_causal, seed,
-                                                 uniforms)
-    return out.reshape(L, B, E), weights
+    res = StochasticTreeAttention.apply(q, k, v, num_samples, block_size, max_logit, is_causal, seed, uniforms, paths,
+                                        bool(return_paths))
+    return (res[0].reshape(L, B, E),) + tuple(res[1:])
 
 
 def tree_attention(
@@ -148,6 +156,7 @@ def tree_attention(
     uniforms: torch.Tensor | None = None,
     return_weights: bool = False,
     causal_mode: str = "auto",
+    paths: torch.Tensor | None = None,
 ):
     """Stochastic tree attention on ``(B, L, H, D)`` tensors.
 
@@ -158,12 +167,14 @@ def tree_attention(
     ``branching=2, leaf_block=1, tree_mode="compat"`` this is the reference
     adapter's stochastic computation (``baselines/treeattn_torch.py:48-90``),
     causal included (``causal_mode="auto"`` selects the reference's causal
-    semantics on that tree; see ``TreeOptions``).
+    semantics on that tree; see ``TreeOptions``).  ``paths`` (non-causal):
+    packed path bits ``(L, B, H, S, path_bytes(L // leaf_block))`` uint8 to
+    replay instead of sampling (``pack_paths``).
     """
     opts = TreeOptions(num_samples=int(num_samples), branching=int(branching), leaf_block=int(leaf_block),
                        tree_mode=tree_mode, causal=bool(causal), causal_mode=causal_mode, scale=softmax_scale,
                        max_logit=float(max_logit), seed=int(seed), layout="bshd")
-    out, weights = TreeAttentionFunction.apply(q, k, v, opts, uniforms)
+    out, weights = TreeAttentionFunction.apply(q, k, v, opts, uniforms, paths)
     return (out, weights) if return_weights else out
 
 

@@ -406,4 +406,79 @@ int ta_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* 
                        "haar_keys_adjoint");
 }
 
+// ---- packed path record
+
+static int path_nbits(int64_t NL, int* nbits) {
+  if (NL < 1 || NL > ((int64_t)1 << 31) || (NL & (NL - 1)))
+    return fail(TA_ERR_INVALID, "num_leaf_blocks must be a power of two in [1, 2^31] (got %lld)", (long long)NL);
+  int t = 0;
+  while (((int64_t)1 << t) < NL) ++t;
+  *nbits = t;
+  return TA_OK;
+}
+
+static int path_dims(int64_t B, int64_t L, int64_t H, int64_t S) {
+  if (B < 0 || L < 0 || H < 0 || S < 0) return fail(TA_ERR_INVALID, "negative path dimension");
+  if (B * L * H * S >= ((int64_t)1 << 40)) return fail(TA_ERR_UNSUPPORTED, "too many paths");
+  return TA_OK;
+}
+
+int ta_path_bytes(int64_t num_leaf_blocks, int64_t* bytes) {
+  int nb = 0;
+  const int rc = path_nbits(num_leaf_blocks, &nb);
+  if (rc) return rc;
+  if (!bytes) return fail(TA_ERR_INVALID, "NULL output");
+  *bytes = (nb + 7) / 8;
+  return ok();
+}
+
+int ta_pack_paths(const int32_t* leaf, const int64_t* leaf_strides, int64_t B, int64_t L, int64_t H, int64_t S,
+                  int64_t num_leaf_blocks, uint8_t* packed, void* stream) {
+  int nb = 0;
+  int rc = path_nbits(num_leaf_blocks, &nb);
+  if (rc) return rc;
+  rc = path_dims(B, L, H, S);
+  if (rc) return rc;
+  if (B * L * H * S > 0 && nb > 0 && (!leaf || !leaf_strides || !packed))
+    return fail(TA_ERR_INVALID, "NULL pointer");
+  return launch_status(launch_pack_paths(leaf, leaf_strides, B, L, H, S, nb, packed, (hipStream_t)stream),
+                       "pack_paths");
+}
+
+int ta_unpack_paths(const uint8_t* packed, int64_t B, int64_t L, int64_t H, int64_t S, int64_t num_leaf_blocks,
+                    int32_t* leaf, const int64_t* leaf_strides, void* stream) {
+  int nb = 0;
+  int rc = path_nbits(num_leaf_blocks, &nb);
+  if (rc) return rc;
+  rc = path_dims(B, L, H, S);
+  if (rc) return rc;
+  if (B * L * H * S > 0 && (!leaf || !leaf_strides || (nb > 0 && !packed))) return fail(TA_ERR_INVALID, "NULL pointer");
+  return launch_status(launch_unpack_paths(packed, B, L, H, S, nb, leaf, leaf_strides, (hipStream_t)stream),
+                       "unpack_paths");
+}
+
+int ta_replay(const ta_problem* p, const void* q, const uint8_t* packed, float* weights, void* record,
+              void* stream) {
+  Plan P;
+  const int rc = make_plan(p, &P);
+  if (rc) return rc;
+  if (p->causal != TA_CAUSAL_NONE)
+    return fail(TA_ERR_UNSUPPORTED, "path replay is for non-causal problems (as the reference's replay)");
+  if (!q || !weights || !record || !aligned16(q) || !aligned16(record) || (P.geo.T > 0 && !packed))
+    return fail(TA_ERR_INVALID, "q/packed/weights/record must be device pointers (q, record 16-byte aligned)");
+  return launch_status(launch_sample(P, q, nullptr, 0, weights, (char*)record, (hipStream_t)stream, packed),
+                       "replay");
+}
+
+int ta_forward_replay(const ta_problem* p, const void* q, const void* k, const void* v, const uint8_t* packed,
+                      void* out, float* weights, void* record, void* workspace, void* stream) {
+  int rc = ta_pool(p, k, record, stream);
+  if (rc) return rc;
+  rc = ta_replay(p, q, packed, weights, record, stream);
+  if (rc) return rc;
+  rc = ta_bucket(p, record, stream);
+  if (rc) return rc;
+  return ta_leaf_forward(p, q, k, v, out, record, workspace, stream);
+}
+
 }  // extern "C"

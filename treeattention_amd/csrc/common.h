@@ -458,6 +458,18 @@ __device__ __host__ inline Philox4 philox4x32_10(uint64_t ctr, uint64_t seed) {
   return o;
 }
 
+// Packed path bits (bit p = p-th root-to-leaf bit, bytes least-significant
+// bit first) <-> leaf block id (those bits most-significant first), nbits in
+// [1, 31]: one bit reversal of the little-endian word.
+__device__ __forceinline__ uint32_t path_leaf(const uint8_t* p, int nbits, int nbytes) {
+  uint32_t w = 0;
+  for (int k = 0; k < nbytes; ++k) w |= (uint32_t)p[k] << (8 * k);
+  return nbits > 0 ? __builtin_bitreverse32(w) >> (32 - nbits) : 0u;
+}
+__device__ __forceinline__ uint32_t leaf_path_word(uint32_t id, int nbits) {
+  return nbits > 0 ? __builtin_bitreverse32(id << (32 - nbits)) : 0u;
+}
+
 __device__ __host__ inline float word_to_uniform(uint32_t x) {
   return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f);
 }

@@ -25,8 +25,15 @@ struct Plan {
 hipError_t launch_pool(const Plan& P, const void* k, char* rec, hipStream_t st);
 hipError_t launch_fill_uniforms(uint64_t seed, int64_t n, float* out, hipStream_t st);
 // sample.hip
+// paths (optional): packed path bits (L, B, H, S, bytes) whose directions
+// replace the Gumbel-max decisions (non-causal problems)
 hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
-                         float* weights, char* rec, hipStream_t st);
+                         float* weights, char* rec, hipStream_t st, const uint8_t* paths = nullptr);
+// paths.hip (packed path bits; leaf ids with (b, l, h, s) strides st)
+hipError_t launch_pack_paths(const int* leaf, const int64_t* st, int64_t B, int64_t L, int64_t H, int64_t S,
+                             int nbits, uint8_t* packed, hipStream_t stream);
+hipError_t launch_unpack_paths(const uint8_t* packed, int64_t B, int64_t L, int64_t H, int64_t S, int nbits,
+                               int* leaf, const int64_t* st, hipStream_t stream);
 // sample_ref.hip (reference causal mode)
 hipError_t launch_ref_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
                              float* weights, char* rec, hipStream_t st);

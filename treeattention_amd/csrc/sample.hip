@@ -26,7 +26,7 @@ namespace ta {
 
 struct SampleArgs {
   Geo geo;
-  int L, H, S, causal, coff;  // coff = N - L: causal offset of query positions
+  int B, L, H, S, causal, coff;  // coff = N - L: causal offset of query positions
   float maxhalf;
   const void* q;
   int64_t qsb, qsl, qsh;
@@ -41,6 +41,8 @@ struct SampleArgs {
   int* slot_leaf;
   float* slot_weight;
   int* slot_count;
+  const uint8_t* paths;  // replay: packed path bits (L, B, H, S, nbytes), else null
+  int nbits, nbytes;
 };
 
 constexpr int kLevelCols = 256;          // child columns of one level pass
@@ -162,7 +164,8 @@ __device__ __forceinline__ float uniform_at(const float* U, uint64_t seed, int64
 
 // kB: branching known at compile time (2 or 4), or 0 for the runtime value.
 // kNI: (query, sample) items per thread, >= 64 * S / 256.
-template <typename E, int D, int kB, int kNI>
+// kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
+template <typename E, int D, int kB, int kNI, bool kReplay>
 __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
@@ -212,6 +215,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   // trees) the last Philox block stay in registers
   const int nitems = kQueryTile * S;
   int node[kNI], iq[kNI], is[kNI], iblk[kNI];
+  uint32_t rleaf[kNI];  // replay: the given leaf block of each item
   int64_t ubase[kNI];
   float acc[kNI];
   constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
@@ -227,6 +231,9 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     const int l = l0 + min(iq[k], nq - 1);
     iblk[k] = (l + a.coff) / G.LB;
     ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
+    rleaf[k] = 0u;
+    if (kReplay && iq[k] < kQueryTile)
+      rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * S + is[k]) * a.nbytes, a.nbits, a.nbytes);
   }
 #pragma unroll
   for (int k = 0; k < kNC; ++k) {
@@ -341,6 +348,20 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
           float se = 0.f;
           for (int j = 0; j < b; ++j) se += fast_exp2((clampf(xr[j], a.maxhalf) - mx) * kLog2e);
           lse = mx + fast_log2(se) * kLn2;
+        }
+        if constexpr (kReplay) {  // the given digit, its log-prob (non-causal)
+          const int jr = (int)((rleaf[k] >> (lb * (T - 1 - d))) & (uint32_t)(b - 1));
+          float xj = 0.f;
+          if constexpr (kB != 0) {
+#pragma unroll
+            for (int j = 0; j < kB; ++j)
+              if (j == jr) xj = x[j];
+          } else {
+            xj = clampf(xr[jr], a.maxhalf);
+          }
+          node[k] = (node[k] << lb) + jr;
+          acc[k] += xj - lse;
+          continue;
         }
         bool onb = false;
         int js = 0;
@@ -469,9 +490,13 @@ int sample_smem(const Plan& P) {
 
 template <typename E, int D, int kB, int kNI>
 static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
-                              char* rec, hipStream_t st) {
+                              char* rec, hipStream_t st, const uint8_t* paths) {
   SampleArgs a;
   a.geo = P.geo;
+  a.B = (int)P.B;
+  a.paths = paths;
+  a.nbits = P.geo.T * P.geo.lb;
+  a.nbytes = (a.nbits + 7) / 8;
   a.L = (int)P.L;
   a.H = (int)P.H;
   a.S = (int)P.S;
@@ -496,47 +521,48 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.slot_weight = (float*)(rec + P.rec.slot_weight);
   a.slot_count = (int*)(rec + P.rec.slot_count);
   const int smem = sample_smem(P);
-  hipError_t e = hipFuncSetAttribute((const void*)sample_kernel<E, D, kB, kNI>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sample_kernel<E, D, kB, kNI>), dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH),
-                     dim3(256), smem, st, a);
-  return hipGetLastError();
+  auto launch = [&](auto kern) -> hipError_t {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH), dim3(256), smem, st, a);
+    return hipGetLastError();
+  };
+  return paths ? launch(sample_kernel<E, D, kB, kNI, true>) : launch(sample_kernel<E, D, kB, kNI, false>);
 }
 
 template <typename E, int D>
 static hipError_t sample_b(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
-                           hipStream_t st) {
+                           hipStream_t st, const uint8_t* pa) {
   static_assert(kMaxSamples * kQueryTile / 256 == 16, "items per thread");
   const bool few = P.S <= 16;  // 64 * S / 256 <= 4 items per thread
   switch (P.geo.b) {
-    case 2: return few ? sample_impl<E, D, 2, 4>(P, q, U, seed, w, rec, st)
-                       : sample_impl<E, D, 2, 16>(P, q, U, seed, w, rec, st);
-    case 4: return few ? sample_impl<E, D, 4, 4>(P, q, U, seed, w, rec, st)
-                       : sample_impl<E, D, 4, 16>(P, q, U, seed, w, rec, st);
-    default: return few ? sample_impl<E, D, 0, 4>(P, q, U, seed, w, rec, st)
-                        : sample_impl<E, D, 0, 16>(P, q, U, seed, w, rec, st);
+    case 2: return few ? sample_impl<E, D, 2, 4>(P, q, U, seed, w, rec, st, pa)
+                       : sample_impl<E, D, 2, 16>(P, q, U, seed, w, rec, st, pa);
+    case 4: return few ? sample_impl<E, D, 4, 4>(P, q, U, seed, w, rec, st, pa)
+                       : sample_impl<E, D, 4, 16>(P, q, U, seed, w, rec, st, pa);
+    default: return few ? sample_impl<E, D, 0, 4>(P, q, U, seed, w, rec, st, pa)
+                        : sample_impl<E, D, 0, 16>(P, q, U, seed, w, rec, st, pa);
   }
 }
 
 template <typename E>
 static hipError_t sample_d(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
-                           hipStream_t st) {
+                           hipStream_t st, const uint8_t* pa) {
   switch (P.D) {
-    case 32: return sample_b<E, 32>(P, q, U, seed, w, rec, st);
-    case 64: return sample_b<E, 64>(P, q, U, seed, w, rec, st);
-    case 96: return sample_b<E, 96>(P, q, U, seed, w, rec, st);
-    default: return sample_b<E, 128>(P, q, U, seed, w, rec, st);
+    case 32: return sample_b<E, 32>(P, q, U, seed, w, rec, st, pa);
+    case 64: return sample_b<E, 64>(P, q, U, seed, w, rec, st, pa);
+    case 96: return sample_b<E, 96>(P, q, U, seed, w, rec, st, pa);
+    default: return sample_b<E, 128>(P, q, U, seed, w, rec, st, pa);
   }
 }
 
 hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
-                         char* rec, hipStream_t st) {
+                         char* rec, hipStream_t st, const uint8_t* paths) {
   if (P.p.causal == TA_CAUSAL_REFERENCE) return launch_ref_sample(P, q, U, seed, weights, rec, st);
   switch (P.p.dtype) {
-    case TA_F32: return sample_d<float>(P, q, U, seed, weights, rec, st);
-    case TA_BF16: return sample_d<bf16>(P, q, U, seed, weights, rec, st);
-    default: return sample_d<f16>(P, q, U, seed, weights, rec, st);
+    case TA_F32: return sample_d<float>(P, q, U, seed, weights, rec, st, paths);
+    case TA_BF16: return sample_d<bf16>(P, q, U, seed, weights, rec, st, paths);
+    default: return sample_d<f16>(P, q, U, seed, weights, rec, st, paths);
   }
 }
 

@@ -164,13 +164,16 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = None):
-    """Forward only: returns ``(out, weights, record)``."""
+def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = None,
+                 paths: torch.Tensor | None = None):
+    """Forward only: returns ``(out, weights, record)``.  With ``paths``
+    (packed path bits, ``(L, B, H, S, path_bytes)`` uint8, see
+    ``pack_paths``) the given paths are replayed instead of sampled."""
     lib = _lib.load()
     D = q.shape[-1]
     if D not in _HEAD_DIMS:
         q, k, v, opts = _pad_heads(q, k, v, opts)
-        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+        out, weights, record = tree_forward(q, k, v, opts, uniforms, paths)
         return out[..., :D], weights, record
     q, k, v = _prep(q), _prep(k), _prep(v)
     prob = make_problem(q, k, v, opts)
@@ -189,10 +192,26 @@ def tree_forward(q, k, v, opts: TreeOptions, uniforms: torch.Tensor | None = Non
             raise ValueError(
                 f"uniforms must be a contiguous float32 (B, L, H, S, T, b) tensor on {q.device}, "
                 f"leading dims {expect}; got {tuple(uniforms.shape)} {uniforms.dtype}")
+    if paths is not None:
+        if uniforms is not None:
+            raise ValueError("give either uniforms or paths, not both")
+        if prob.causal != _lib.TA_CAUSAL_NONE:
+            raise ValueError("path replay is for non-causal attention (as the reference's replay)")
+        nl = prob.N // prob.leaf_block
+        expect = (prob.L, prob.B, prob.H, opts.num_samples, path_bytes(nl))
+        if (paths.dtype != torch.uint8 or not paths.is_contiguous() or paths.device != q.device
+                or tuple(paths.shape) != expect):
+            raise ValueError(f"paths must be a contiguous uint8 {expect} tensor on {q.device}; "
+                             f"got {tuple(paths.shape)} {paths.dtype}")
     with torch.cuda.device(q.device):
-        _lib.check(lib.ta_forward(ctypes.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(uniforms),
-                                  ctypes.c_uint64(opts.seed & 0xFFFFFFFFFFFFFFFF), out.data_ptr(),
-                                  weights.data_ptr(), record.data_ptr(), work.data_ptr(), _stream(q.device)))
+        if paths is not None:
+            _lib.check(lib.ta_forward_replay(ctypes.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             paths.data_ptr(), out.data_ptr(), weights.data_ptr(),
+                                             record.data_ptr(), work.data_ptr(), _stream(q.device)))
+        else:
+            _lib.check(lib.ta_forward(ctypes.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(uniforms),
+                                      ctypes.c_uint64(opts.seed & 0xFFFFFFFFFFFFFFFF), out.data_ptr(),
+                                      weights.data_ptr(), record.data_ptr(), work.data_ptr(), _stream(q.device)))
     return out, weights, record
 
 
@@ -221,11 +240,11 @@ def tree_backward(q, k, v, weights, record, grad_out, opts: TreeOptions):
 
 
 class TreeAttentionFunction(torch.autograd.Function):
-    """``apply(q, k, v, opts, uniforms=None) -> (out, weights)``."""
+    """``apply(q, k, v, opts, uniforms=None, paths=None) -> (out, weights)``."""
 
     @staticmethod
-    def forward(ctx, q, k, v, opts: TreeOptions, uniforms=None):
-        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+    def forward(ctx, q, k, v, opts: TreeOptions, uniforms=None, paths=None):
+        out, weights, record = tree_forward(q, k, v, opts, uniforms, paths)
         ctx.save_for_backward(q, k, v, weights, record)
         ctx.opts = opts
         ctx.mark_non_differentiable(weights)
@@ -236,7 +255,7 @@ class TreeAttentionFunction(torch.autograd.Function):
         del grad_weights
         q, k, v, weights, record = ctx.saved_tensors
         dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, ctx.opts)
-        return dq, dk, dv, None, None
+        return dq, dk, dv, None, None, None
 
 
 class StochasticTreeAttention(torch.autograd.Function):
@@ -244,14 +263,20 @@ class StochasticTreeAttention(torch.autograd.Function):
 
     ``apply(q (L,B,H,D), k (N-1,B,H,D) heap-ordered node keys, v (N,B,H,D),
     num_samples, block_size, max_logit, is_causal=False, seed=0,
-    uniforms=None) -> (out (L,B,H,D), weights (L,B,H,S) float32)``, gradients
-    ``(dq, dk, dv, None, ...)`` (``_autograd.py:645-707,860``).  ``block_size``
-    (the reference's query streaming) does not change results and is
-    accepted for compatibility.  Edge cases follow ``_autograd.py:660-683``.
+    uniforms=None, paths=None, return_paths=False) -> (out (L,B,H,D),
+    weights (L,B,H,S) float32)``, gradients ``(dq, dk, dv, None, ...)``
+    (``_autograd.py:645-707,860``).  ``block_size`` (the reference's query
+    streaming) does not change results and is accepted for compatibility.
+    Edge cases follow ``_autograd.py:660-683``.  ``paths``: packed path bits
+    ``(L, B, H, S, ceil(log2(N)/8))`` uint8 (the reference's saved path
+    record, ``_autograd.py:68-90``) to replay instead of sampling
+    (non-causal); ``return_paths=True`` adds the forward's own packed paths
+    as a third output.
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, num_samples, block_size=256, max_logit=1e3, is_causal=False, seed=0, uniforms=None):
+    def forward(ctx, q, k, v, num_samples, block_size=256, max_logit=1e3, is_causal=False, seed=0, uniforms=None,
+                paths=None, return_paths=False):
         del block_size
         num_leaves = v.shape[0]
         if num_samples <= 0:
@@ -266,23 +291,36 @@ class StochasticTreeAttention(torch.autograd.Function):
                 weights = torch.ones((*q.shape[:-1], 1), device=q.device, dtype=q.dtype)
             ctx.save_for_backward(q, k, v)
             ctx.mark_non_differentiable(weights)
-            return out, weights
+            if not return_paths:
+                return out, weights
+            packed = torch.zeros((*q.shape[:-1], int(num_samples), 0), device=q.device, dtype=torch.uint8)
+            ctx.mark_non_differentiable(packed)
+            return out, weights, packed
+        if paths is not None and is_causal:
+            raise ValueError("path replay is for non-causal attention (as the reference's replay)")
         opts = TreeOptions(num_samples=int(num_samples), branching=2, leaf_block=1, tree_mode="nodekeys",
                            causal=bool(is_causal), max_logit=float(max_logit), seed=int(seed), layout="lbhd")
-        out, weights, record = tree_forward(q, k, v, opts, uniforms)
+        out, weights, record = tree_forward(q, k, v, opts, uniforms, paths)
         ctx.save_for_backward(q, k, v, weights, record)
         ctx.opts = opts
+        packed = None
+        if return_paths:
+            leaves, _ = record_views(q, k, v, opts, record)
+            packed = pack_paths(leaves, num_leaves, layout="blhs")
         if is_causal and q.shape[0] > num_samples:
             # hybrid: the first num_samples queries are exact; the reference returns the
             # sample weights of the other rows only (_tree_mha.py:379-413)
             weights = weights[num_samples:]
         ctx.mark_non_differentiable(weights)
-        return out, weights
+        if packed is None:
+            return out, weights
+        ctx.mark_non_differentiable(packed)
+        return out, weights, packed
 
     @staticmethod
-    def backward(ctx, grad_out, grad_weights):
-        del grad_weights
-        nones = (None,) * 6
+    def backward(ctx, grad_out, grad_weights, *grad_paths):
+        del grad_weights, grad_paths
+        nones = (None,) * 8
         if ctx.num_leaves <= 1:
             q, k, v = ctx.saved_tensors
             dv = torch.zeros_like(v)
@@ -468,3 +506,57 @@ def record_views(q, k, v, opts: TreeOptions, record: torch.Tensor):
     n_sum = prob.B * prob.H * ns * prob.D
     summaries = record[so:so + 4 * n_sum].view(torch.float32).view(prob.B * prob.H, ns, prob.D)
     return leaves, summaries
+
+
+# ---------------------------------------------------------------------------
+# Packed path record (_autograd.py:68-90,179-216): per (position, batch, head,
+# sample) the root-to-leaf directions, bit p (p = 0 at the root) in byte p//8
+# at bit p%8; in a b-ary tree each level's digit takes log2(b) bits, high bit
+# first, so the bits spell the leaf block id most-significant bit first.
+
+
+def path_bytes(num_leaf_blocks: int) -> int:
+    """Bytes per packed path, ``ceil(log2(num_leaf_blocks) / 8)`` (``_autograd.py:68-70``)."""
+    out = ctypes.c_int64(0)
+    _lib.check(_lib.load().ta_path_bytes(int(num_leaf_blocks), ctypes.byref(out)))
+    return out.value
+
+
+def pack_paths(leaves: torch.Tensor, num_leaf_blocks: int, layout: str = "lbhs") -> torch.Tensor:
+    """Leaf block ids (int32, 4-D; dims ordered as ``layout``, ``"lbhs"`` (the
+    reference's ``current_nodes``) or ``"blhs"`` (the record's leaves)) ->
+    packed paths ``(L, B, H, S, path_bytes)`` uint8."""
+    if leaves.dtype != torch.int32 or leaves.dim() != 4 or not leaves.is_cuda:
+        raise ValueError("leaves must be a 4-D int32 GPU tensor")
+    if layout not in ("lbhs", "blhs"):
+        raise ValueError(f"layout must be 'lbhs' or 'blhs', got {layout!r}")
+    if layout == "lbhs":
+        L, B, H, S = leaves.shape
+        st = leaves.stride()
+        strides = (st[1], st[0], st[2], st[3])
+    else:
+        B, L, H, S = leaves.shape
+        strides = leaves.stride()
+    nb = path_bytes(num_leaf_blocks)
+    out = torch.empty((L, B, H, S, nb), device=leaves.device, dtype=torch.uint8)
+    st4 = (ctypes.c_int64 * 4)(*strides)
+    with torch.cuda.device(leaves.device):
+        _lib.check(_lib.load().ta_pack_paths(leaves.data_ptr(), st4, B, L, H, S, int(num_leaf_blocks),
+                                              out.data_ptr(), _stream(leaves.device)))
+    return out
+
+
+def unpack_paths(packed: torch.Tensor, num_leaf_blocks: int) -> torch.Tensor:
+    """Packed paths ``(L, B, H, S, path_bytes)`` uint8 -> leaf block ids ``(L, B, H, S)`` int32."""
+    nb = path_bytes(num_leaf_blocks)
+    if packed.dtype != torch.uint8 or packed.dim() != 5 or packed.shape[4] != nb or not packed.is_cuda:
+        raise ValueError(f"packed must be a (L, B, H, S, {nb}) uint8 GPU tensor")
+    packed = packed.contiguous()
+    L, B, H, S, _ = packed.shape
+    leaves = torch.empty((L, B, H, S), device=packed.device, dtype=torch.int32)
+    st = leaves.stride()
+    st4 = (ctypes.c_int64 * 4)(st[1], st[0], st[2], st[3])
+    with torch.cuda.device(packed.device):
+        _lib.check(_lib.load().ta_unpack_paths(packed.data_ptr(), B, L, H, S, int(num_leaf_blocks),
+                                                leaves.data_ptr(), st4, _stream(packed.device)))
+    return leaves
