@@ -147,6 +147,21 @@ int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
                const float* uniforms, uint64_t seed, void* out, float* weights,
                void* record, void* workspace, void* stream);
 
+/* Streaming forward of the deterministic mode for bfloat16 / float16 inputs:
+ * out = W V with _deterministic_attention's weights (_tree_mha.py:286-318)
+ * without materializing the (L, N) weights (memory O(L D)).  q and out
+ * (batch, position, head) strides, v (batch, token, head), `knodes` the N-1
+ * heap-ordered node keys in the input type with (batch, node, head) strides;
+ * head dim 32/64/96/128, contiguous; other strides multiples of 8 elements.
+ * N = 2^T with 64 <= N <= TA_DET_MAX_LEAVES.  Causal (leaves n <= l): `lse`
+ * (B, H, L) float32, optional, receives each row's log-normalizer.  Replaces
+ * _deterministic_attention's forward (_tree_mha.py:271-321) on the adapter's
+ * path (baselines/treeattn_torch.py:55-90), which returns no weights. */
+int ta_det_stream_forward(int dtype, const void* q, const int64_t* q_strides, const void* knodes,
+                          const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
+                          const int64_t* o_strides, float* lse, int64_t B, int64_t L, int64_t H,
+                          int64_t D, int64_t N, int causal, void* stream);
+
 /* Packed path record of the reference (_autograd.py:68-90,179-216), the
  * stable on-device format of the sampled paths: per (position, batch, head,
  * sample) the root-to-leaf directions as a bit string, bit p (p = 0 at the

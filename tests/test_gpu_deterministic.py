@@ -167,3 +167,57 @@ def test_deterministic_mode_is_bitwise_reproducible():
     o1, w1 = ta.hierarchical_attention(q, k, v, num_heads=H, is_causal=True, mode="deterministic")
     o2, w2 = ta.hierarchical_attention(q, k, v, num_heads=H, is_causal=True, mode="deterministic")
     assert torch.equal(o1, o2) and torch.equal(w1, w2)
+
+
+STREAM_CASES = [
+    # N (= L), D, dtype, causal
+    (64, 64, torch.bfloat16, False),
+    (64, 32, torch.float16, True),
+    (256, 128, torch.bfloat16, True),
+    (1024, 96, torch.float16, False),
+    (1024, 64, torch.bfloat16, True),
+    (4096, 128, torch.bfloat16, False),
+]
+
+
+@pytest.mark.parametrize("N,D,dtype,causal", STREAM_CASES)
+def test_streaming_forward_matches_restatement(N, D, dtype, causal):
+    """The streaming forward (no (L, N) weights) against the float64 restatement, with the node keys
+    rounded to the input type as the kernel reads them."""
+    from treeattention_amd.function import det_stream_forward
+
+    B, H = 1, 2
+    print(f"[case] stream fwd N={N} D={D} {dtype} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(N + D)
+    q = torch.randn(B, N, H, D, generator=g).to(dtype)
+    kn = (torch.randn(N - 1, B, H, D, generator=g) / D ** 0.5).to(dtype)
+    v = torch.randn(B, N, H, D, generator=g).to(dtype)
+    out = det_stream_forward(q.to(DEV), kn.to(DEV), v.to(DEV), causal)
+    torch.cuda.synchronize()
+    qt, kt, vt = (torch.tensor(x.double().numpy()) for x in (q.permute(1, 0, 2, 3), kn, v.permute(1, 0, 2, 3)))
+    ref, _ = R.deterministic_attention(qt, kt, vt, causal)
+    assert out.shape == q.shape and out.dtype == dtype
+    assert rel(f64(out).transpose(1, 0, 2, 3), ref.numpy()) < 2e-2
+
+
+def test_streaming_adapter_path_long_causal(monkeypatch):
+    """Adapter deterministic path at S = 2048 (streaming forward, recomputed backward) against the
+    float64 restatement with the oracle's Haar node keys."""
+    monkeypatch.delenv("TREEATTN_NUM_SAMPLES", raising=False)
+    for var in ("TREEATTN_BRANCHING", "TREEATTN_LEAF_BLOCK", "TREEATTN_TREE_MODE"):
+        monkeypatch.delenv(var, raising=False)
+    B, S, H, D = 1, 2048, 2, 64
+    print(f"[case] adapter deterministic streaming S={S}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    q, k, v, dout = (torch.randn(B, S, H, D, generator=g).to(torch.bfloat16) for _ in range(4))
+    qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    out = ta.attn_fn(qg, kg, vg, True, None)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    q64, k64, v64, d64 = (x.double().numpy().transpose(1, 0, 2, 3) for x in (q, k, v, dout))
+    out_r, _, dq_r, dkn_r, dv_r = _oracle(q64, O.haar_inorder(k64), v64, d64, True)
+    tr = lambda a: a.transpose(1, 0, 2, 3)  # noqa: E731
+    assert rel(f64(out), tr(out_r)) < 2e-2
+    assert rel(f64(qg.grad), tr(dq_r)) < 2e-2
+    assert rel(f64(kg.grad), tr(O.haar_inorder_adjoint(dkn_r))) < 2e-2
+    assert rel(f64(vg.grad), tr(dv_r)) < 2e-2

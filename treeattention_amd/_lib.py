@@ -71,6 +71,7 @@ EXPORTS = (
     "ta_det_grad",
     "ta_haar_keys",
     "ta_haar_keys_adjoint",
+    "ta_det_stream_forward",
     "ta_path_bytes",
     "ta_pack_paths",
     "ta_unpack_paths",
@@ -123,6 +124,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_haar_keys.argtypes = [ctypes.c_int, vp, i64p, vp, i64, i64, i64, i64, vp]
     lib.ta_haar_keys_adjoint.restype = ctypes.c_int
     lib.ta_haar_keys_adjoint.argtypes = [ctypes.c_int, vp, vp, i64p, i64, i64, i64, i64, vp]
+    lib.ta_det_stream_forward.restype = ctypes.c_int
+    lib.ta_det_stream_forward.argtypes = [ctypes.c_int, vp, i64p, vp, i64p, vp, i64p, vp, i64p, vp, i64, i64, i64,
+                                          i64, i64, ctypes.c_int, vp]
     lib.ta_path_bytes.restype = ctypes.c_int
     lib.ta_path_bytes.argtypes = [i64, i64p]
     lib.ta_pack_paths.restype = ctypes.c_int

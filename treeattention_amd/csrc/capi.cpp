@@ -406,6 +406,35 @@ int ta_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* 
                        "haar_keys_adjoint");
 }
 
+int ta_det_stream_forward(int dtype, const void* q, const int64_t* q_strides, const void* knodes,
+                          const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
+                          const int64_t* o_strides, float* lse, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                          int causal, void* stream) {
+  int T = 0;
+  const int rc = det_depth(N, &T);
+  if (rc) return rc;
+  if (dtype != TA_BF16 && dtype != TA_F16)
+    return fail(TA_ERR_UNSUPPORTED, "the streaming deterministic forward takes bfloat16 / float16 inputs");
+  if (N < 64) return fail(TA_ERR_UNSUPPORTED, "the streaming deterministic forward needs N >= 64 (got %lld)", (long long)N);
+  if (D != 32 && D != 64 && D != 96 && D != 128)
+    return fail(TA_ERR_UNSUPPORTED, "head dim must be 32, 64, 96 or 128 (got %lld)", (long long)D);
+  if (B < 0 || L < 0 || H < 0 || B * H >= 65536 || L >= ((int64_t)1 << 30))
+    return fail(TA_ERR_INVALID, "bad batch / length / head count");
+  if (B * L * H == 0) return ok();
+  if (!q || !knodes || !v || !out || !q_strides || !k_strides || !v_strides || !o_strides)
+    return fail(TA_ERR_INVALID, "NULL pointer");
+  const void* al[] = {q, knodes, v, out};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  const int64_t* st[] = {q_strides, k_strides, v_strides, o_strides};
+  for (const int64_t* s : st)
+    for (int i = 0; i < 3; ++i)
+      if (s[i] % 8) return fail(TA_ERR_INVALID, "strides must be multiples of 8 elements");
+  return launch_status(launch_det_stream_fwd(dtype, q, q_strides, knodes, k_strides, v, v_strides, out, o_strides, lse,
+                                             (int)B, (int)L, (int)H, (int)D, T, causal != 0, (hipStream_t)stream),
+                       "det_stream_forward");
+}
+
 // ---- packed path record
 
 static int path_nbits(int64_t NL, int* nbits) {

@@ -320,6 +320,18 @@ __device__ __forceinline__ s16x4 tr_read4(const E* X, int rs, int row, int col) 
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp)(X + row * rs + col));
 }
 
+// An MFMA operand fragment of k = 8 values from the row-major [k][n] LDS tile
+// X (row stride rs): rows k0a..k0a+3 then k0b..k0b+3 of column n0 + lane % 16,
+// through two transposing reads.
+template <typename E>
+__device__ __forceinline__ typename Mfma<E>::frag tr_frag(const E* X, int rs, int k0a, int k0b, int n0, int lane) {
+  const int j = lane & 15;
+  const s16x4 lo = tr_read4(X, rs, k0a + (j >> 2), n0 + 4 * (j & 3));
+  const s16x4 hi = tr_read4(X, rs, k0b + (j >> 2), n0 + 4 * (j & 3));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Mfma<E>::frag, v);
+}
+
 // A-operand fragment of a (head dims x keys) product read from the row-major
 // [key][dim] LDS tile X: tile md = 2p + e, row m <-> dim 32p + 8(m/4) + 4e +
 // m%4 (so that the product's output gives each lane eight consecutive dims),

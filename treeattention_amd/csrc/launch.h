@@ -59,6 +59,11 @@ hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* 
 hipError_t launch_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* ks, int B, int H, int D,
                                     int N, int T, hipStream_t st);
 
+// det_stream.hip (deterministic mode, streaming forward for 16-bit inputs)
+hipError_t launch_det_stream_fwd(int dtype, const void* q, const int64_t* qs, const void* kn, const int64_t* ks,
+                                 const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse, int B,
+                                 int L, int H, int D, int T, int causal, hipStream_t st);
+
 // Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
 // variant fits in 160 KiB.
 int leaf_fwd_smem(const Plan& P);

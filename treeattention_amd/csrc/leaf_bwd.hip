@@ -277,16 +277,6 @@ struct PairRows {
   }
 };
 
-// An MFMA operand fragment of k = 8 values: rows k0a..k0a+3 then k0b..k0b+3.
-template <typename E>
-__device__ __forceinline__ typename Mfma<E>::frag tr_frag(const E* X, int rs, int k0a, int k0b, int n0, int lane) {
-  const int j = lane & 15;
-  const s16x4 lo = tr_read4(X, rs, k0a + (j >> 2), n0 + 4 * (j & 3));
-  const s16x4 hi = tr_read4(X, rs, k0b + (j >> 2), n0 + 4 * (j & 3));
-  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(typename Mfma<E>::frag, v);
-}
-
 template <typename E, int D, int LBP>
 __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
   static_assert(sizeof(E) == 2, "16-bit inputs");

@@ -353,21 +353,51 @@ def _on_device(*ts) -> None:
             raise ValueError("tree attention runs on HIP device tensors; got a tensor on " + str(t.device))
 
 
-def det_forward(q, k, v, causal: bool):
-    """``q (L,B,H,D)``, node keys ``k (N-1,B,H,D)``, ``v (N,B,H,D)`` -> ``(out (L,B,H,D)
-    in v's dtype, W (B,H,L,N) float32)``."""
-    _on_device(q, k, v)
+def det_weights(q, k, N: int, causal: bool):
+    """Exact leaf weights ``W (B,H,L,N)`` float32 of ``q (L,B,H,D)`` and node keys ``k (N-1,B,H,D)``."""
+    _on_device(q, k)
     lib = _lib.load()
     L, B, H, _ = q.shape
-    N = v.shape[0]
     qf, kf = _bh(q), _bh(k)
     X = torch.matmul(qf, kf.transpose(-1, -2).contiguous())  # (B, H, L, N-1)
     W = torch.empty((B, H, L, N), device=q.device, dtype=torch.float32)
     with torch.cuda.device(q.device):
         _lib.check(lib.ta_det_weights(X.data_ptr(), N - 1, W.data_ptr(), N, B * H * L, L, N, int(bool(causal)),
                                       _stream(q.device)))
+    return W
+
+
+def det_forward(q, k, v, causal: bool):
+    """``q (L,B,H,D)``, node keys ``k (N-1,B,H,D)``, ``v (N,B,H,D)`` -> ``(out (L,B,H,D)
+    in v's dtype, W (B,H,L,N) float32)``."""
+    _on_device(q, k, v)
+    W = det_weights(q, k, v.shape[0], causal)
     out = torch.matmul(W.to(v.dtype), v.permute(1, 2, 0, 3).contiguous())  # weights cast to v's dtype (:318)
     return out.permute(2, 0, 1, 3), W
+
+
+def det_stream_supported(q: torch.Tensor, N: int) -> bool:
+    """Whether the streaming forward covers this case: 16-bit inputs, 64 <= N <= 32768, kernel head dim."""
+    return q.dtype in (torch.bfloat16, torch.float16) and 64 <= N <= 32768 and q.shape[-1] in _HEAD_DIMS
+
+
+def det_stream_forward(q, kn, v, causal: bool, layout: str = "bshd"):
+    """Exact tree attention without the ``(L, N)`` weights: ``q``, ``v`` in ``layout`` (``"bshd"`` or
+    ``"lbhd"``), node keys ``kn (N-1, B, H, D)`` in q's dtype -> ``out`` (q's layout and dtype)."""
+    _on_device(q, kn, v)
+    lib = _lib.load()
+    q, v, kn = _prep(q), _prep(v), _prep(kn.to(q.dtype))
+    B, L = _bl(q, layout)
+    H, D = q.shape[2], q.shape[3]
+    N = v.shape[1] if layout == "bshd" else v.shape[0]
+    out = torch.empty_like(q)
+    qs, vs, os_ = ((ctypes.c_int64 * 3)(*_strides(t, layout)) for t in (q, v, out))
+    ks = (ctypes.c_int64 * 3)(kn.stride(1), kn.stride(0), kn.stride(2))
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ta_det_stream_forward(_DTYPES[q.dtype], q.data_ptr(), qs, kn.data_ptr(), ks, v.data_ptr(), vs,
+                                             out.data_ptr(), os_, None, B, L, H, D, N, int(bool(causal)),
+                                             _stream(q.device)))
+    return out
 
 
 def det_backward(q, k, v, W, grad_out, causal: bool):
@@ -476,16 +506,22 @@ class DeterministicAdapterAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, causal):
         kt = haar_node_keys(k)
+        ctx.causal = bool(causal)
+        if det_stream_supported(q, k.shape[1]):
+            # 16-bit inputs: streaming forward, nothing of size L x N is kept; the backward
+            # recomputes the weights
+            ctx.save_for_backward(q, k, v, kt)
+            return det_stream_forward(q, kt, v, causal)
         ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
         out, W = det_forward(ql, kt, vl, causal)
         ctx.save_for_backward(q, k, v, kt, W)
-        ctx.causal = bool(causal)
         return out.permute(1, 0, 2, 3).contiguous()
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, kt, W = ctx.saved_tensors
+        q, k, v, kt, *rest = ctx.saved_tensors
         ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
+        W = rest[0] if rest else det_weights(ql, kt, v.shape[1], ctx.causal)
         dq, dkt, dv = det_backward(ql, kt, vl, W, grad_out.permute(1, 0, 2, 3), ctx.causal)
         dk = haar_node_keys_adjoint(dkt, k)
         return dq.permute(1, 0, 2, 3), dk, dv.permute(1, 0, 2, 3), None
