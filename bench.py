@@ -121,11 +121,11 @@ def cpu_baseline(cfg) -> dict:
 
 def det_main(args) -> int:
     """Deterministic mode on the reference tree: fwd+bwd of the adapter path (Haar keys, exact
-    weights over every leaf), plus the leaf-weight row kernel timed alone for its HBM roofline."""
+    weights over every leaf; 16-bit inputs stream, no (L, N) buffer), plus the streaming forward
+    kernel timed alone for its roofline (nominal FLOPs of the two products, q K_nodes^T and W V)."""
     import torch
 
-    from treeattention_amd import _lib
-    from treeattention_amd.function import DeterministicAdapterAttention
+    from treeattention_amd.function import DeterministicAdapterAttention, det_stream_forward, haar_node_keys
 
     B, L, H, D, dts, _, _, _, causal, kind = CONFIGS[args.config]
     dtype = getattr(torch, dts)
@@ -160,18 +160,15 @@ def det_main(args) -> int:
         step()
     step_ms = timed(step, args.steps)
     fwd_ms = timed(fwd, args.steps)
-    # the leaf-weight row kernel alone: reads the N-1 node logits, writes the N weights of each row
-    lib = _lib.load()
-    rows, N = B * H * L, L
-    X = torch.randn((rows, N - 1), device=dev, dtype=torch.float32, generator=gen)
-    W = torch.empty((rows, N), device=dev, dtype=torch.float32)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    run = lambda: _lib.check(lib.ta_det_weights(X.data_ptr(), N - 1, W.data_ptr(), N, rows, L, N, int(causal),  # noqa: E731
-                                                stream))
-    run()
-    kern_ms = timed(run, max(3, args.steps))
-    alg_bytes = rows * (4 * (N - 1) + 4 * N)
-    achieved = alg_bytes / (kern_ms / 1e3) / 1e9
+    with torch.no_grad():
+        kn = haar_node_keys(k).to(dtype)
+        qd, vd = q.detach(), v.detach()
+        run = lambda: det_stream_forward(qd, kn, vd, causal)  # noqa: E731
+        run()
+        kern_ms = timed(run, max(3, args.steps))
+    N = L
+    flops = 4.0 * B * H * L * N * D * (0.5 if causal else 1.0)
+    achieved = flops / (kern_ms / 1e3) / 1e12
     line = {
         "metric": "deterministic tree-attn fwd+bwd ms & queries/s (reference tree, exact weights)",
         "value": round(B * L / (step_ms / 1e3), 1),
@@ -189,8 +186,8 @@ def det_main(args) -> int:
         "data": "synthetic: q,k,v,dout ~ N(0,1) (torch.Generator seed 0)",
         "config": {"workload": f"{args.config} shape, deterministic mode, reference tree (Haar keys)", "batch": B,
                    "seq_len": L, "heads": H, "head_dim": D, "causal": causal},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "det_weights",
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_PEAK[dts], "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_PEAK[dts], 4), "traffic": None, "kernel": "det_stream_forward",
                      "kernel_ms": round(kern_ms, 4)},
     }
     print(json.dumps(line))

@@ -162,6 +162,25 @@ int ta_det_stream_forward(int dtype, const void* q, const int64_t* q_strides, co
                           const int64_t* o_strides, float* lse, int64_t B, int64_t L, int64_t H,
                           int64_t D, int64_t N, int causal, void* stream);
 
+/* Its backward, streaming as well (no (L, N) buffer), in two parts:
+ *  - here: `dq_sub` (B, H, L, D) float32, the gradient through the nodes of
+ *    every 64-leaf subtree; `dknodes` (N-1, B, H, D) float32 rows of those
+ *    nodes; `dv` (value strides, input type); `chunk_totals` (B, H, L, N/64)
+ *    float32, each row's sum of dL/dlog w over each 64-leaf chunk;
+ *  - by the caller: the N/64 - 1 top nodes are the deterministic mode on a
+ *    coarse tree whose leaves are the chunks: X_top = q K_top^T, then
+ *    ta_det_grad with W = chunk_totals, dW = 1, non-causal gives G_top;
+ *    dq = dq_sub + G_top K_top, dknodes[top] = G_top^T q.
+ * Causal needs `lse` (from ta_det_stream_forward) and `delta` (B, H, L) =
+ * rowwise dout . out.  Replaces the autograd of _deterministic_attention
+ * (_tree_mha.py:271-321) on the adapter's path. */
+int ta_det_stream_backward(int dtype, const void* q, const int64_t* q_strides, const void* grad_out,
+                           const int64_t* g_strides, const void* knodes, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const float* lse, const float* delta,
+                           float* dq_sub, float* chunk_totals, float* dknodes, void* dv,
+                           const int64_t* dv_strides, int64_t B, int64_t L, int64_t H, int64_t D,
+                           int64_t N, int causal, void* stream);
+
 /* Packed path record of the reference (_autograd.py:68-90,179-216), the
  * stable on-device format of the sampled paths: per (position, batch, head,
  * sample) the root-to-leaf directions as a bit string, bit p (p = 0 at the

@@ -221,3 +221,26 @@ def test_streaming_adapter_path_long_causal(monkeypatch):
     assert rel(f64(qg.grad), tr(dq_r)) < 2e-2
     assert rel(f64(kg.grad), tr(O.haar_inorder_adjoint(dkn_r))) < 2e-2
     assert rel(f64(vg.grad), tr(dv_r)) < 2e-2
+
+
+@pytest.mark.parametrize("N,D,dtype,causal", STREAM_CASES + [(128, 64, torch.bfloat16, True)])
+def test_streaming_backward_matches_restatement(N, D, dtype, causal):
+    """The streaming backward (subtree kernels + coarse top tree) against float64 autograd of the
+    restatement, node keys rounded to the input type as the kernels read them."""
+    from treeattention_amd.function import det_stream_backward, det_stream_forward
+
+    B, H = 1, 2
+    print(f"[case] stream bwd N={N} D={D} {dtype} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(3 * N + D)
+    q = torch.randn(B, N, H, D, generator=g).to(dtype)
+    kn = (torch.randn(N - 1, B, H, D, generator=g) / D ** 0.5).to(dtype)
+    v, dout = (torch.randn(B, N, H, D, generator=g).to(dtype) for _ in range(2))
+    qg, kg, vg, dg = (x.to(DEV) for x in (q, kn, v, dout))
+    out, lse = det_stream_forward(qg, kg, vg, causal, return_lse=True)
+    dq, dkn, dv = det_stream_backward(qg, kg, vg, dg, out, lse, causal)
+    torch.cuda.synchronize()
+    lbhd = lambda t: t.permute(1, 0, 2, 3)  # noqa: E731
+    out_r, _, dq_r, dk_r, dv_r = _oracle(*(x.double().numpy() for x in (lbhd(q), kn, lbhd(v), lbhd(dout))), causal)
+    assert rel(f64(lbhd(dq)), dq_r) < 2e-2, rel(f64(lbhd(dq)), dq_r)
+    assert rel(f64(dkn), dk_r) < 2e-2, rel(f64(dkn), dk_r)
+    assert rel(f64(lbhd(dv)), dv_r) < 2e-2, rel(f64(lbhd(dv)), dv_r)

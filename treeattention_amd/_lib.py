@@ -72,6 +72,7 @@ EXPORTS = (
     "ta_haar_keys",
     "ta_haar_keys_adjoint",
     "ta_det_stream_forward",
+    "ta_det_stream_backward",
     "ta_path_bytes",
     "ta_pack_paths",
     "ta_unpack_paths",
@@ -127,6 +128,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_det_stream_forward.restype = ctypes.c_int
     lib.ta_det_stream_forward.argtypes = [ctypes.c_int, vp, i64p, vp, i64p, vp, i64p, vp, i64p, vp, i64, i64, i64,
                                           i64, i64, ctypes.c_int, vp]
+    lib.ta_det_stream_backward.restype = ctypes.c_int
+    lib.ta_det_stream_backward.argtypes = [ctypes.c_int, vp, i64p, vp, i64p, vp, i64p, vp, i64p, vp, vp, vp, vp, vp,
+                                           vp, i64p, i64, i64, i64, i64, i64, ctypes.c_int, vp]
     lib.ta_path_bytes.restype = ctypes.c_int
     lib.ta_path_bytes.argtypes = [i64, i64p]
     lib.ta_pack_paths.restype = ctypes.c_int

@@ -435,6 +435,38 @@ int ta_det_stream_forward(int dtype, const void* q, const int64_t* q_strides, co
                        "det_stream_forward");
 }
 
+int ta_det_stream_backward(int dtype, const void* q, const int64_t* q_strides, const void* grad_out,
+                           const int64_t* g_strides, const void* knodes, const int64_t* k_strides, const void* v,
+                           const int64_t* v_strides, const float* lse, const float* delta, float* dq_sub,
+                           float* chunk_totals, float* dknodes, void* dv, const int64_t* dv_strides, int64_t B,
+                           int64_t L, int64_t H, int64_t D, int64_t N, int causal, void* stream) {
+  int T = 0;
+  const int rc = det_depth(N, &T);
+  if (rc) return rc;
+  if (dtype != TA_BF16 && dtype != TA_F16)
+    return fail(TA_ERR_UNSUPPORTED, "the streaming deterministic backward takes bfloat16 / float16 inputs");
+  if (N < 64) return fail(TA_ERR_UNSUPPORTED, "the streaming deterministic backward needs N >= 64 (got %lld)", (long long)N);
+  if (D != 32 && D != 64 && D != 96 && D != 128)
+    return fail(TA_ERR_UNSUPPORTED, "head dim must be 32, 64, 96 or 128 (got %lld)", (long long)D);
+  if (B < 0 || L < 0 || H < 0 || B * H >= 65536 || L >= ((int64_t)1 << 30))
+    return fail(TA_ERR_INVALID, "bad batch / length / head count");
+  if (B * H == 0) return ok();
+  if (!q || !grad_out || !knodes || !v || !dq_sub || !chunk_totals || !dknodes || !dv || !q_strides || !g_strides ||
+      !k_strides || !v_strides || !dv_strides || (causal && (!lse || !delta)))
+    return fail(TA_ERR_INVALID, "NULL pointer");
+  const void* al[] = {q, grad_out, knodes, v, dv};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  const int64_t* st[] = {q_strides, g_strides, k_strides, v_strides, dv_strides};
+  for (const int64_t* s : st)
+    for (int i = 0; i < 3; ++i)
+      if (s[i] % 8) return fail(TA_ERR_INVALID, "strides must be multiples of 8 elements");
+  return launch_status(launch_det_stream_bwd(dtype, q, q_strides, grad_out, g_strides, knodes, k_strides, v,
+                                             v_strides, lse, delta, dq_sub, chunk_totals, dknodes, dv, dv_strides,
+                                             (int)B, (int)L, (int)H, (int)D, T, causal != 0, (hipStream_t)stream),
+                       "det_stream_backward");
+}
+
 // ---- packed path record
 
 static int path_nbits(int64_t NL, int* nbits) {

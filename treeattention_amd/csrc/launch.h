@@ -64,6 +64,12 @@ hipError_t launch_det_stream_fwd(int dtype, const void* q, const int64_t* qs, co
                                  const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse, int B,
                                  int L, int H, int D, int T, int causal, hipStream_t st);
 
+// det_stream_bwd.hip (its backward: dq and node-key gradients of the 64-leaf subtrees, dv)
+hipError_t launch_det_stream_bwd(int dtype, const void* q, const int64_t* qs, const void* gout, const int64_t* gs,
+                                 const void* kn, const int64_t* ks, const void* v, const int64_t* vs, const float* lse,
+                                 const float* delta, float* dq, float* achunk, float* dkn, void* dv,
+                                 const int64_t* dvs, int B, int L, int H, int D, int T, int causal, hipStream_t st);
+
 // Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
 // variant fits in 160 KiB.
 int leaf_fwd_smem(const Plan& P);

@@ -381,9 +381,10 @@ def det_stream_supported(q: torch.Tensor, N: int) -> bool:
     return q.dtype in (torch.bfloat16, torch.float16) and 64 <= N <= 32768 and q.shape[-1] in _HEAD_DIMS
 
 
-def det_stream_forward(q, kn, v, causal: bool, layout: str = "bshd"):
+def det_stream_forward(q, kn, v, causal: bool, layout: str = "bshd", return_lse: bool = False):
     """Exact tree attention without the ``(L, N)`` weights: ``q``, ``v`` in ``layout`` (``"bshd"`` or
-    ``"lbhd"``), node keys ``kn (N-1, B, H, D)`` in q's dtype -> ``out`` (q's layout and dtype)."""
+    ``"lbhd"``), node keys ``kn (N-1, B, H, D)`` in q's dtype -> ``out`` (q's layout and dtype), and
+    with ``return_lse`` the causal log-normalizer ``(B, H, L)`` float32 (None when not causal)."""
     _on_device(q, kn, v)
     lib = _lib.load()
     q, v, kn = _prep(q), _prep(v), _prep(kn.to(q.dtype))
@@ -391,13 +392,56 @@ def det_stream_forward(q, kn, v, causal: bool, layout: str = "bshd"):
     H, D = q.shape[2], q.shape[3]
     N = v.shape[1] if layout == "bshd" else v.shape[0]
     out = torch.empty_like(q)
+    lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32) if causal else None
     qs, vs, os_ = ((ctypes.c_int64 * 3)(*_strides(t, layout)) for t in (q, v, out))
     ks = (ctypes.c_int64 * 3)(kn.stride(1), kn.stride(0), kn.stride(2))
     with torch.cuda.device(q.device):
         _lib.check(lib.ta_det_stream_forward(_DTYPES[q.dtype], q.data_ptr(), qs, kn.data_ptr(), ks, v.data_ptr(), vs,
-                                             out.data_ptr(), os_, None, B, L, H, D, N, int(bool(causal)),
+                                             out.data_ptr(), os_, _ptr(lse), B, L, H, D, N, int(bool(causal)),
                                              _stream(q.device)))
-    return out
+    return (out, lse) if return_lse else out
+
+
+def det_stream_backward(q, kn, v, grad_out, out, lse, causal: bool, layout: str = "bshd"):
+    """Gradients of ``det_stream_forward``: ``(dq (q's layout and dtype), dkn (N-1, B, H, D) float32,
+    dv (v's layout and dtype))``.  The 64-leaf subtrees' part runs in the library's streaming
+    kernels; the ``N/64 - 1`` top nodes are the exact mode on a coarse tree whose leaves are the
+    chunks (``ta_det_grad`` on the chunk totals, two small products)."""
+    _on_device(q, kn, v, grad_out)
+    lib = _lib.load()
+    q, v, grad_out, kn = _prep(q), _prep(v), _prep(grad_out), _prep(kn.to(q.dtype))
+    B, L = _bl(q, layout)
+    H, D = q.shape[2], q.shape[3]
+    N = v.shape[1] if layout == "bshd" else v.shape[0]
+    NC = N // 64
+    dev = q.device
+    delta = None
+    if causal:
+        d = (grad_out.float() * out.float()).sum(-1)  # dout . out per row
+        delta = (d.permute(0, 2, 1) if layout == "bshd" else d.permute(1, 2, 0)).contiguous()  # (B, H, L)
+    dq_sub = torch.empty((B, H, L, D), device=dev, dtype=torch.float32)
+    tot = torch.empty((B, H, L, NC), device=dev, dtype=torch.float32)
+    dkn = torch.empty((N - 1, B, H, D), device=dev, dtype=torch.float32)
+    dv = torch.empty_like(v)
+    qs, gs, vs, dvs = ((ctypes.c_int64 * 3)(*_strides(t, layout)) for t in (q, grad_out, v, dv))
+    ks = (ctypes.c_int64 * 3)(kn.stride(1), kn.stride(0), kn.stride(2))
+    st = _stream(dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.ta_det_stream_backward(_DTYPES[q.dtype], q.data_ptr(), qs, grad_out.data_ptr(), gs,
+                                              kn.data_ptr(), ks, v.data_ptr(), vs, _ptr(lse), _ptr(delta),
+                                              dq_sub.data_ptr(), tot.data_ptr(), dkn.data_ptr(), dv.data_ptr(), dvs,
+                                              B, L, H, D, N, int(bool(causal)), st))
+        qf = (q.permute(0, 2, 1, 3) if layout == "bshd" else q.permute(1, 2, 0, 3)).float()  # (B, H, L, D)
+        if NC >= 2:
+            kt = kn[:NC - 1].float().permute(1, 2, 0, 3)  # (B, H, NC-1, D)
+            X = torch.matmul(qf, kt.transpose(-1, -2).contiguous()).contiguous()  # top-node logits
+            ones = torch.ones_like(tot)
+            _lib.check(lib.ta_det_grad(X.data_ptr(), NC - 1, tot.data_ptr(), ones.data_ptr(), NC, B * H * L, NC, 0,
+                                       st))
+            dq_sub += torch.matmul(X, kt)
+            dkn[:NC - 1] = torch.matmul(X.transpose(-1, -2), qf).permute(2, 0, 1, 3)
+    dq = (dq_sub.permute(0, 2, 1, 3) if layout == "bshd" else dq_sub.permute(2, 0, 1, 3)).to(q.dtype)
+    return dq, dkn, dv
 
 
 def det_backward(q, k, v, W, grad_out, causal: bool):
@@ -508,10 +552,13 @@ class DeterministicAdapterAttention(torch.autograd.Function):
         kt = haar_node_keys(k)
         ctx.causal = bool(causal)
         if det_stream_supported(q, k.shape[1]):
-            # 16-bit inputs: streaming forward, nothing of size L x N is kept; the backward
-            # recomputes the weights
-            ctx.save_for_backward(q, k, v, kt)
-            return det_stream_forward(q, kt, v, causal)
+            # 16-bit inputs: streaming forward and backward, nothing of size L x N
+            kt = kt.to(q.dtype)
+            out, lse = det_stream_forward(q, kt, v, causal, return_lse=True)
+            ctx.stream = True
+            ctx.save_for_backward(q, k, v, kt, out, *([lse] if lse is not None else []))
+            return out
+        ctx.stream = False
         ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
         out, W = det_forward(ql, kt, vl, causal)
         ctx.save_for_backward(q, k, v, kt, W)
@@ -519,9 +566,12 @@ class DeterministicAdapterAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, kt, *rest = ctx.saved_tensors
+        if ctx.stream:
+            q, k, v, kt, out, *lse = ctx.saved_tensors
+            dq, dkt, dv = det_stream_backward(q, kt, v, grad_out, out, lse[0] if lse else None, ctx.causal)
+            return dq, haar_node_keys_adjoint(dkt, k), dv, None
+        q, k, v, kt, W = ctx.saved_tensors
         ql, vl = q.permute(1, 0, 2, 3), v.permute(1, 0, 2, 3)
-        W = rest[0] if rest else det_weights(ql, kt, v.shape[1], ctx.causal)
         dq, dkt, dv = det_backward(ql, kt, vl, W, grad_out.permute(1, 0, 2, 3), ctx.causal)
         dk = haar_node_keys_adjoint(dkt, k)
         return dq.permute(1, 0, 2, 3), dk, dv.permute(1, 0, 2, 3), None
