@@ -266,9 +266,13 @@ int ta_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t
  * node m, p = m + 1, w = lowest set bit of p:
  * key = (mean k[p-w, p) - mean k[p, p+w)) / 2.  Replaces
  * haar_internal_node_keys (_treeattn_common.py:54-86) as read in heap order
- * by the op (_tree_mha.py:288-291). */
-int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, int64_t B, int64_t H,
-                 int64_t D, int64_t N, void* stream);
+ * by the op (_tree_mha.py:288-291).  With `workspace` (float scratch of
+ * ta_haar_workspace_bytes, 16-byte aligned) the keys come from a block-sum
+ * pyramid in O(N) work per (batch, head) and dim; with NULL, from per-node
+ * window sums (O(N log N), no scratch). */
+int ta_haar_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t N, int64_t* bytes);
+int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, float* workspace,
+                 int64_t B, int64_t H, int64_t D, int64_t N, void* stream);
 
 /* dk (B, N, H, D, strides dk_strides, fully overwritten) = transpose of
  * ta_haar_keys applied to dkey (N-1, B, H, D) float.  Replaces the autograd of

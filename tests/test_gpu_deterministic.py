@@ -244,3 +244,20 @@ def test_streaming_backward_matches_restatement(N, D, dtype, causal):
     assert rel(f64(lbhd(dq)), dq_r) < 2e-2, rel(f64(lbhd(dq)), dq_r)
     assert rel(f64(dkn), dk_r) < 2e-2, rel(f64(dkn), dk_r)
     assert rel(f64(lbhd(dv)), dv_r) < 2e-2, rel(f64(lbhd(dv)), dv_r)
+
+
+@pytest.mark.parametrize("N,D,dtype", [(2, 32, torch.float32), (64, 96, torch.bfloat16), (128, 64, torch.float32),
+                                       (4096, 128, torch.float32), (8192, 36, torch.float16)])
+def test_haar_pyramid_matches_oracle(N, D, dtype):
+    """The block-sum pyramid (segment levels in LDS, then the levels over segment sums) against the
+    oracle's in-order Haar transform read in heap order."""
+    from treeattention_amd.function import haar_node_keys
+
+    B, H = 1, 2
+    print(f"[case] haar pyramid N={N} D={D} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(N + D)
+    k = torch.randn(B, N, H, D, generator=g).to(dtype)
+    kt = haar_node_keys(k.to(DEV))
+    torch.cuda.synchronize()
+    ref = O.haar_inorder(k.double().numpy().transpose(1, 0, 2, 3))
+    assert rel(f64(kt), ref) < 1e-6

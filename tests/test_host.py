@@ -144,7 +144,9 @@ def test_deterministic_entry_points_validate_before_launching():
     assert lib.ta_det_weights(None, 15, None, 16, 0, 1, 16, 0, None) == 0  # no rows: nothing to do
     assert lib.ta_det_weights(None, 3, None, 16, 16, 16, 16, 0, None) == 1  # row stride too small
     ks = (ctypes.c_int64 * 3)(0, 0, 0)
-    assert lib.ta_haar_keys(_lib.TA_BF16, None, ks, None, 1, 1, 32, 12, None) == 1
+    assert lib.ta_haar_keys(_lib.TA_BF16, None, ks, None, None, 1, 1, 32, 12, None) == 1
+    nb = ctypes.c_int64(0)
+    assert lib.ta_haar_workspace_bytes(2, 3, 64, 4096, ctypes.byref(nb)) == 0 and nb.value == 4 * 2 * 3 * 32 * 64
 
 
 def test_cpu_tensors_are_rejected_not_computed():

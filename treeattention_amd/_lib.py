@@ -69,6 +69,7 @@ EXPORTS = (
     "ta_backward",
     "ta_det_weights",
     "ta_det_grad",
+    "ta_haar_workspace_bytes",
     "ta_haar_keys",
     "ta_haar_keys_adjoint",
     "ta_det_stream_forward",
@@ -122,7 +123,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_det_grad.restype = ctypes.c_int
     lib.ta_det_grad.argtypes = [vp, i64, vp, vp, i64, i64, i64, ctypes.c_int, vp]
     lib.ta_haar_keys.restype = ctypes.c_int
-    lib.ta_haar_keys.argtypes = [ctypes.c_int, vp, i64p, vp, i64, i64, i64, i64, vp]
+    lib.ta_haar_keys.argtypes = [ctypes.c_int, vp, i64p, vp, vp, i64, i64, i64, i64, vp]
+    lib.ta_haar_workspace_bytes.restype = ctypes.c_int
+    lib.ta_haar_workspace_bytes.argtypes = [i64, i64, i64, i64, i64p]
     lib.ta_haar_keys_adjoint.restype = ctypes.c_int
     lib.ta_haar_keys_adjoint.argtypes = [ctypes.c_int, vp, vp, i64p, i64, i64, i64, i64, vp]
     lib.ta_det_stream_forward.restype = ctypes.c_int

@@ -387,12 +387,22 @@ static int haar_check(int dtype, const void* a, const void* b, const int64_t* s,
   return TA_OK;
 }
 
-int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, int64_t B, int64_t H, int64_t D,
-                 int64_t N, void* stream) {
+int ta_haar_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t N, int64_t* bytes) {
+  if (!bytes) return fail(TA_ERR_INVALID, "NULL output");
+  if (B < 1 || H < 1 || N < 2 || (N & (N - 1)) || D < 4 || D % 4)
+    return fail(TA_ERR_INVALID, "need B, H >= 1, N = 2^T >= 2 and D a multiple of 4");
+  *bytes = 4 * haar_workspace_floats((int)B, (int)H, (int)D, (int)N);
+  return ok();
+}
+
+int ta_haar_keys(int dtype, const void* k, const int64_t* k_strides, float* out, float* workspace, int64_t B,
+                 int64_t H, int64_t D, int64_t N, void* stream) {
   const int rc = haar_check(dtype, k, out, k_strides, B, H, D, N);
   if (rc) return rc;
-  return launch_status(
-      launch_haar_keys(dtype, k, k_strides, out, (int)B, (int)H, (int)D, (int)N, (hipStream_t)stream), "haar_keys");
+  if (workspace && ((uintptr_t)workspace & 15)) return fail(TA_ERR_INVALID, "workspace must be 16-byte aligned");
+  return launch_status(launch_haar_keys(dtype, k, k_strides, out, workspace, (int)B, (int)H, (int)D, (int)N,
+                                        (hipStream_t)stream),
+                       "haar_keys");
 }
 
 int ta_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* dk_strides, int64_t B, int64_t H,

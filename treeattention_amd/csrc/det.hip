@@ -247,6 +247,73 @@ __global__ __launch_bounds__(256) void haar_keys_kernel(const E* __restrict__ k,
                             (sl_[3] - sr_[3]) * f);
 }
 
+// The same keys from a block-sum pyramid, O(N D) work per (batch, head): at
+// level l (w = 2^l) the nodes are p = (2j + 1) w, with key (BS_l[2j] -
+// BS_l[2j+1]) / 2w for the block sums BS_l of w keys, and BS_{l+1}[j] =
+// BS_l[2j] + BS_l[2j+1].  haar_seg_kernel runs the levels inside segments of
+// kHaarSeg tokens in LDS (one workgroup per segment and (batch, head)) and
+// leaves each segment's sum; haar_top_kernel runs the levels above on the
+// segment sums (one workgroup per (batch, head) and 16 head dims).
+constexpr int kHaarSeg = 128;
+constexpr int kHaarTopDims = 16;
+
+template <typename E>
+__global__ __launch_bounds__(256) void haar_seg_kernel(const E* __restrict__ k, int64_t sb, int64_t sl, int64_t sh,
+                                                       float* __restrict__ out, float* __restrict__ segsum, int B,
+                                                       int H, int D, int seg) {
+  extern __shared__ __align__(16) float buf[];  // [seg][D]
+  const int s = blockIdx.x, bh = blockIdx.y, bb = bh / H, h = bh - bb * H;
+  const int t0 = s * seg, D4 = D / 4;
+  for (int e = threadIdx.x; e < seg * D4; e += 256) {
+    const int tok = e / D4, d0 = (e - tok * D4) * 4;
+    const E* src = k + bb * sb + (int64_t)(t0 + tok) * sl + h * sh + d0;
+    *(float4*)(buf + tok * D + d0) = make_float4(tof(src[0]), tof(src[1]), tof(src[2]), tof(src[3]));
+  }
+  __syncthreads();
+  for (int lv = 0; (2 << lv) <= seg; ++lv) {
+    const int w = 1 << lv, npair = seg >> (lv + 1);
+    const float f = 0.5f / (float)w;
+    for (int e = threadIdx.x; e < npair * D4; e += 256) {
+      const int j = e / D4, d0 = (e - j * D4) * 4;
+      float* pa = buf + (2 * j * w) * D + d0;
+      const float4 a = *(const float4*)pa, b = *(const float4*)(pa + w * D);
+      const int64_t m = (int64_t)t0 + (2 * j + 1) * w - 1;
+      *(float4*)(out + ((m * B + bb) * H + h) * D + d0) =
+          make_float4((a.x - b.x) * f, (a.y - b.y) * f, (a.z - b.z) * f, (a.w - b.w) * f);
+      *(float4*)pa = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+    __syncthreads();
+  }
+  if (segsum)
+    for (int e = threadIdx.x; e < D4; e += 256)
+      *(float4*)(segsum + ((int64_t)bh * gridDim.x + s) * D + 4 * e) = *(const float4*)(buf + 4 * e);
+}
+
+__global__ __launch_bounds__(256) void haar_top_kernel(const float* __restrict__ segsum, float* __restrict__ out,
+                                                       int B, int H, int D, int nseg, int seg) {
+  extern __shared__ __align__(16) float tb[];  // [nseg][kHaarTopDims]
+  const int bh = blockIdx.x, bb = bh / H, h = bh - bb * H, dc = blockIdx.y * kHaarTopDims;
+  for (int e = threadIdx.x; e < nseg * kHaarTopDims; e += 256) {
+    const int sg = e / kHaarTopDims, d = e - sg * kHaarTopDims;
+    tb[e] = dc + d < D ? segsum[((int64_t)bh * nseg + sg) * D + dc + d] : 0.f;
+  }
+  __syncthreads();
+  for (int lv = 0; (2 << lv) <= nseg; ++lv) {
+    const int ws = 1 << lv, npair = nseg >> (lv + 1);
+    const int64_t wt = (int64_t)ws * seg;  // block width in tokens
+    const float f = 0.5f / (float)wt;
+    for (int e = threadIdx.x; e < npair * kHaarTopDims; e += 256) {
+      const int j = e / kHaarTopDims, d = e - j * kHaarTopDims;
+      float* pa = tb + (2 * j * ws) * kHaarTopDims + d;
+      const float a = pa[0], b = pa[ws * kHaarTopDims];
+      const int64_t m = (2 * j + 1) * wt - 1;
+      if (dc + d < D) out[((m * B + bb) * H + h) * D + dc + d] = (a - b) * f;
+      pa[0] = a + b;
+    }
+    __syncthreads();
+  }
+}
+
 // dk[b, t, h, :] = sum over the levels l of +-dkey[m_l] / 2^(l+1): at level l
 // leaf t lies in the left (+) or right (-) span of exactly one coefficient,
 // p_l = (t >> (l+1) << (l+1)) + 2^l.  One thread per (t, b, h, 4 dims).
@@ -297,22 +364,41 @@ hipError_t launch_det_grad(float* XG, int64_t ldx, const float* W, const float* 
 }
 
 template <typename E>
-static hipError_t haar_keys_t(const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
-                              hipStream_t st) {
+static hipError_t haar_keys_t(const void* k, const int64_t* ks, float* out, float* segsum, int B, int H, int D,
+                              int N, hipStream_t st) {
   const int64_t total = (int64_t)(N - 1) * B * H * (D / 4);
   if (total == 0) return hipSuccess;
+  const int seg = N < kHaarSeg ? N : kHaarSeg, nseg = N / seg;
+  const int smem = seg * D * 4;
+  if (segsum && smem <= 160 * 1024 && nseg * kHaarTopDims * 4 <= 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)haar_seg_kernel<E>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(haar_seg_kernel<E>, dim3((unsigned)nseg, (unsigned)(B * H)), dim3(256), smem, st,
+                       (const E*)k, ks[0], ks[1], ks[2], out, nseg > 1 ? segsum : nullptr, B, H, D, seg);
+    e = hipGetLastError();
+    if (e != hipSuccess || nseg == 1) return e;
+    hipLaunchKernelGGL(haar_top_kernel, dim3((unsigned)(B * H), (unsigned)((D + kHaarTopDims - 1) / kHaarTopDims)),
+                       dim3(256), nseg * kHaarTopDims * 4, st, segsum, out, B, H, D, nseg, seg);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(haar_keys_kernel<E>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (const E*)k, ks[0],
                      ks[1], ks[2], out, B, H, D, N);
   return hipGetLastError();
 }
 
-hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
-                            hipStream_t st) {
+hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, float* segsum, int B, int H,
+                            int D, int N, hipStream_t st) {
   switch (dtype) {
-    case TA_F32: return haar_keys_t<float>(k, ks, out, B, H, D, N, st);
-    case TA_BF16: return haar_keys_t<bf16>(k, ks, out, B, H, D, N, st);
-    default: return haar_keys_t<f16>(k, ks, out, B, H, D, N, st);
+    case TA_F32: return haar_keys_t<float>(k, ks, out, segsum, B, H, D, N, st);
+    case TA_BF16: return haar_keys_t<bf16>(k, ks, out, segsum, B, H, D, N, st);
+    default: return haar_keys_t<f16>(k, ks, out, segsum, B, H, D, N, st);
   }
+}
+
+int64_t haar_workspace_floats(int B, int H, int D, int N) {
+  const int seg = N < kHaarSeg ? N : kHaarSeg;
+  return (int64_t)B * H * (N / seg) * D;
 }
 
 template <typename E>

@@ -54,8 +54,9 @@ hipError_t launch_det_weights(const float* X, int64_t ldx, float* W, int64_t ldw
                               int causal, hipStream_t st);
 hipError_t launch_det_grad(float* XG, int64_t ldx, const float* W, const float* dW, int64_t ldw, int64_t rows, int N,
                            int T, int causal, hipStream_t st);
-hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, int B, int H, int D, int N,
-                            hipStream_t st);
+hipError_t launch_haar_keys(int dtype, const void* k, const int64_t* ks, float* out, float* segsum, int B, int H,
+                            int D, int N, hipStream_t st);
+int64_t haar_workspace_floats(int B, int H, int D, int N);
 hipError_t launch_haar_keys_adjoint(int dtype, const float* dkey, void* dk, const int64_t* ks, int B, int H, int D,
                                     int N, int T, hipStream_t st);
 

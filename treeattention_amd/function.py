@@ -523,8 +523,11 @@ def haar_node_keys(k: torch.Tensor) -> torch.Tensor:
     k = _prep(k)
     out = torch.empty((N - 1, B, H, D), device=k.device, dtype=torch.float32)
     ks = (ctypes.c_int64 * 3)(*_strides(k, "bshd"))
+    nbytes = ctypes.c_int64(0)
+    _lib.check(lib.ta_haar_workspace_bytes(B, H, D, N, ctypes.byref(nbytes)))
+    work = torch.empty(nbytes.value // 4, device=k.device, dtype=torch.float32)
     with torch.cuda.device(k.device):
-        _lib.check(lib.ta_haar_keys(_DTYPES[k.dtype], k.data_ptr(), ks, out.data_ptr(), B, H, D, N,
+        _lib.check(lib.ta_haar_keys(_DTYPES[k.dtype], k.data_ptr(), ks, out.data_ptr(), work.data_ptr(), B, H, D, N,
                                     _stream(k.device)))
     return out
 
