@@ -76,11 +76,13 @@ __device__ __forceinline__ int chunk_node(int cix, int r, int tt) {
   return -1;
 }
 
+// Row padding of 8 elements keeps the chunk-major kernel at D <= 64 within
+// 80 KiB of LDS (two workgroups per CU).
 template <typename E, int D>
 struct DbTiles {
-  static constexpr int RS = D + 16;          // row stride (elements) of K / V / q / dout tiles
+  static constexpr int RS = D + 8;           // row stride (elements) of K / V / q / dout tiles
   static constexpr int XS = kDbCols + 4;     // float row stride of the logit (then dW) tile
-  static constexpr int PS = kDbLeaves + 16;  // row stride (elements) of the W / G tiles
+  static constexpr int PS = kDbLeaves + 8;   // row stride (elements) of the W / G tiles
 };
 
 // Stage chunk r's node-key columns and value rows into Ks / Vs (all threads).
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void det_bwd_q_kernel(DetBwdArgs a) {
 
 // dv and the chunk's subtree rows of dk: one workgroup per (chunk, batch*head).
 template <typename E, int D>
-__global__ __launch_bounds__(256, 1) void det_bwd_kv_kernel(DetBwdArgs a) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void det_bwd_kv_kernel(DetBwdArgs a) {
   using M = Mfma<E>;
   using TL = DbTiles<E, D>;
   constexpr int RS = TL::RS, XS = TL::XS, PS = TL::PS, NDT = D / 16, KS = D / M::K;
