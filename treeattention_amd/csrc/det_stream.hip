@@ -49,13 +49,14 @@ struct DetStreamArgs {
   int B, L, H, T, causal;
 };
 
+// Eight-element row padding: at D <= 64 three workgroups fit per CU.
 template <typename E, int D>
-__global__ __launch_bounds__(256, 2) void det_stream_fwd_kernel(DetStreamArgs a) {
+__global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void det_stream_fwd_kernel(DetStreamArgs a) {
   using M = Mfma<E>;
   constexpr int KS = D / M::K;
-  constexpr int RS = D + 16;             // LDS row stride (elements) of the K and V tiles
+  constexpr int RS = D + 8;              // LDS row stride (elements) of the K and V tiles
   constexpr int XS = kDsCols + 4;        // float row stride of the logit tile
-  constexpr int PS = kDsLeaves + 16;     // row stride (elements) of the weight tile
+  constexpr int PS = kDsLeaves + 8;      // row stride (elements) of the weight tile
   constexpr int NDT = D / 16;
   __shared__ __align__(16) E Ks[kDsCols * RS];
   __shared__ __align__(16) E Vs[kDsLeaves * RS];
