@@ -475,6 +475,14 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
         }
       }
     }
+    // this chunk's C^T fragments are complete by now (the logit MFMAs above
+    // waited for every earlier load); pin them before the next chunk's loads
+    // go out, so the dq product below waits for neither those loads nor the
+    // G^T stores (vmcnt counts both)
+#pragma unroll
+    for (int i = 0; i < NMD; ++i)
+#pragma unroll
+      for (int ks = 0; ks < KT; ++ks) asm volatile("" ::"v"(at[i][ks]) : "memory");
     if (nd < T) load_af(nd, nc0);
     for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
       const int r = e / (kcols / 8), cc = (e - r * (kcols / 8)) * 8;
