@@ -29,6 +29,9 @@ hipError_t launch_fill_uniforms(uint64_t seed, int64_t n, float* out, hipStream_
 // replace the Gumbel-max decisions (non-causal problems)
 hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t seed,
                          float* weights, char* rec, hipStream_t st, const uint8_t* paths = nullptr);
+// sample_replay.hip
+hipError_t launch_sample_replay(const Plan& P, const void* q, float* weights, char* rec, hipStream_t st,
+                                const uint8_t* paths);
 // paths.hip (packed path bits; leaf ids with (b, l, h, s) strides st)
 hipError_t launch_pack_paths(const int* leaf, const int64_t* st, int64_t B, int64_t L, int64_t H, int64_t S,
                              int nbits, uint8_t* packed, hipStream_t stream);

@@ -1,0 +1,574 @@
+// K2: per-query root-to-leaf path sampling (kernel templates, shared by
+// sample.hip and sample_replay.hip so the two variants compile in parallel).
+//
+// Generalizes _sample_paths_non_causal (_tree_mha.py:78-122) and the
+// treeattn-cuda step kernel (sample_non_causal_paths.cu:54-128) to b-ary trees
+// with leaf blocks.  One workgroup owns 64 consecutive queries of one
+// (batch, head); every thread owns a fixed set of (query, sample) items whose
+// current node and accumulated log-probability stay in registers for the
+// whole walk.  Per depth:
+//   1. the child logits of every node of the level that the tile can reach
+//      are one MFMA product  C_level (rows) x Q^T (64 queries), each wave
+//      taking every fourth 16-row tile of C for all 64 queries, so every
+//      summary row is read once per workgroup.  Summaries are split into
+//      hi + lo parts of the input type so the logits are float-accurate.
+//      The tile lands in LDS as X[query][child].
+//   2. each item reads its node's b child logits from LDS and decides:
+//        logp_j = log_softmax(clamp(x_j, +-max_logit/2))  (+ the causal
+//        correction on the boundary path),
+//        direction = argmax_j(logp_j + g_j), first maximum wins,
+//      with g = -log(-log u) from the caller's uniforms or the counter RNG.
+// Finally each item computes its sample weight (softmax over the query's
+// samples, _tree_mha.py:396-399) and the query's ascending distinct leaf
+// blocks with their summed weights, through LDS.
+#pragma once
+
+#include "launch.h"
+
+namespace ta {
+
+struct SampleArgs {
+  Geo geo;
+  int B, L, H, S, causal, coff;  // coff = N - L: causal offset of query positions
+  float maxhalf;
+  const void* q;
+  int64_t qsb, qsl, qsh;
+  const float* sum32;
+  const void* sum_hi;
+  const void* sum_lo;
+  const float* U;
+  uint64_t seed;
+  float* weights;
+  int64_t wsb, wsl, wsh;
+  int* leaf;
+  int* slot_leaf;
+  float* slot_weight;
+  int* slot_count;
+  const uint8_t* paths;  // replay: packed path bits (L, B, H, S, nbytes), else null
+  int nbits, nbytes;
+};
+
+constexpr int kLevelCols = 256;          // child columns of one level pass
+constexpr int kXS = kLevelCols + 4;      // padded row stride (floats) of the logit tile
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float clampf(float x, float m) { return fminf(fmaxf(x, -m), m); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Child-logit products of one pass: up to kLevelCols/16 column tiles, tile t
+// being the 16 summary rows from row(t) (rows past a level's nodes are zero
+// padding); X[q][16t + c] = q . C[row(t) + c] for all 64 queries of the
+// workgroup.  Wave w computes tiles w, w+4, ...; the next tile's summary
+// fragments are loaded while the current tile's MFMAs run, and the first
+// tile of the next pass is loaded (prefetch) before the caller consumes the
+// current one.
+template <typename E, int D, bool kLo>
+struct LogitPipe {
+  using M = Mfma<E>;
+  using F = typename M::frag;
+  static constexpr int KS = D / M::K;
+  F ah[KS], al[KS];
+  int64_t rmax;  // last valid summary row: tile rows past it read it (results unused)
+
+  __device__ __forceinline__ void load(const E* hi, const E* lo, int64_t row, int lane, F (&h)[KS], F (&l)[KS]) {
+    const int64_t r = min(row + (lane & 15), rmax);
+    const int64_t rb = r * D + M::KPL * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      h[ks] = ld_frag(hi + rb + ks * M::K);
+      if constexpr (kLo) l[ks] = ld_frag(lo + rb + ks * M::K);
+    }
+  }
+
+  template <class RowFn>
+  __device__ __forceinline__ void prefetch(const E* hi, const E* lo, RowFn row, int ntiles, int lane, int w) {
+    if (w < ntiles) load(hi, lo, row(w), lane, ah, al);
+  }
+
+  template <class RowFn>
+  __device__ __forceinline__ void run(const RowFrags<E, D> (&qa)[4], float* Xs, const E* hi, const E* lo, RowFn row,
+                                      int ntiles, int lane, int w) {
+    const int col = lane & 15, g = lane >> 4;
+    for (int ct = w; ct < ntiles; ct += 4) {
+      F nh[KS], nl[KS];
+      if (ct + 4 < ntiles) load(hi, lo, row(ct + 4), lane, nh, nl);
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        f32x4 c = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          c = M::mma(ah[ks], qa[qt].f[ks], c);
+          if constexpr (kLo) c = M::mma(al[ks], qa[qt].f[ks], c);
+        }
+        *(f32x4*)(Xs + (16 * qt + col) * kXS + 16 * ct + 4 * g) = c;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        ah[ks] = nh[ks];
+        if constexpr (kLo) al[ks] = nl[ks];
+      }
+    }
+  }
+};
+
+// The passes of one workgroup, in order: causal boundary batches (the
+// boundary-path children of every depth, 16 column tiles per batch), then
+// every level in chunks of kLevelCols children (causal: only children of
+// nodes that contain a reachable leaf block).
+struct Passes {
+  int T, lb, causal, blk_lo, blk_hi, nbt;  // nbt: causal boundary tiles
+  const Geo* G;
+  int64_t base;                             // first summary row of this (batch, head)
+
+  // depth d's boundary children: columns [c0, c0 + ncols) of level d + 1
+  __device__ __forceinline__ int bc0(int d) const { return (blk_lo >> (lb * (T - d))) << lb; }
+  __device__ __forceinline__ int bcols(int d) const {
+    const int sh = lb * (T - d);
+    return ((blk_hi >> sh) - (blk_lo >> sh) + 1) << lb;
+  }
+  __device__ __forceinline__ int btiles(int d) const { return (bcols(d) + 15) >> 4; }
+  __device__ __forceinline__ int level_cols(int d) const {
+    int n = G->pw[d + 1];
+    if (causal) n = min(n, ((blk_hi >> (lb * (T - d))) + 1) << lb);
+    return n;
+  }
+  __device__ __forceinline__ int nbatch() const { return (nbt + kLevelCols / 16 - 1) / (kLevelCols / 16); }
+  // summary row of global boundary tile t
+  __device__ __forceinline__ int64_t brow(int t) const {
+    int d = 0, t0 = 0;
+    while (t >= t0 + btiles(d)) {
+      t0 += btiles(d);
+      ++d;
+    }
+    return base + G->off[d + 1] + bc0(d) + 16 * (t - t0);
+  }
+};
+
+// Uniform `idx` of the (B, L, H, S, T, b) tensor: from the caller's tensor,
+// else word idx%4 of Philox(idx/4).  The last Philox block is cached per item.
+struct RngCache {
+  uint64_t ctr;
+  uint32_t w0, w1, w2, w3;
+};
+
+__device__ __forceinline__ float uniform_at(const float* U, uint64_t seed, int64_t idx, RngCache& rc) {
+  if (U) return U[idx];
+  const uint64_t ctr = (uint64_t)idx >> 2;
+  if (ctr != rc.ctr) {
+    const Philox4 ph = philox4x32_10(ctr, seed);
+    rc.ctr = ctr;
+    rc.w0 = ph.w[0]; rc.w1 = ph.w[1]; rc.w2 = ph.w[2]; rc.w3 = ph.w[3];
+  }
+  const int wi = (int)(idx & 3);
+  return word_to_uniform(wi == 0 ? rc.w0 : wi == 1 ? rc.w1 : wi == 2 ? rc.w2 : rc.w3);
+}
+
+// kB: branching known at compile time (2 or 4), or 0 for the runtime value.
+// kNI: (query, sample) items per thread, >= 64 * S / 256.
+// kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
+template <typename E, int D, int kB, int kNI, bool kReplay>
+__global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const Geo& G = a.geo;
+  const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int l0 = blockIdx.x * kQueryTile;
+  const int nq = min(kQueryTile, a.L - l0);
+  const int S = a.S, T = G.T, lb = G.lb;
+  const int b = kB ? kB : G.b;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t rows = G.NS;
+  constexpr bool kLo = sizeof(E) == 2;
+
+  float* Xs = (float*)smem;                      // [64][kXS] logits of one level pass
+  float* logA = Xs + kQueryTile * kXS;           // [64][T+1] causal boundary log-mass
+  float* xb = logA + kQueryTile * (T + 1);       // [64][T*b] boundary child logits
+  // after the walk Xs is reused: leaf, log-prob and distinct-leaf key per item
+  int* lf = (int*)Xs;
+  float* lps = Xs + kQueryTile * S;
+  int* fl = (int*)(Xs + 2 * kQueryTile * S);
+
+  // all 64 query rows as MFMA B fragments (rows past nq are zero)
+  RowFrags<E, D> qa[4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int r = 16 * qt + (lane & 15);
+    qa[qt].load(r < nq ? (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh : nullptr, lane >> 4);
+  }
+  const E* hi = (const E*)(sizeof(E) == 2 ? a.sum_hi : (const void*)a.sum32);
+  const E* lo = (const E*)a.sum_lo;
+
+  Passes ps;
+  ps.T = T;
+  ps.lb = lb;
+  ps.causal = a.causal && T > 0;
+  // leaf blocks [0, blk_hi] are reachable from some query of the tile
+  ps.blk_lo = (l0 + a.coff) / G.LB;
+  ps.blk_hi = (l0 + nq - 1 + a.coff) / G.LB;
+  ps.G = &G;
+  ps.base = (int64_t)bh * rows;
+  ps.nbt = 0;
+  if (ps.causal)
+    for (int d = 0; d < T; ++d) ps.nbt += ps.btiles(d);
+  const int nbatch = ps.causal ? ps.nbatch() : 0;
+
+  // items: i = tid + 256 k -> (query i / S, sample i % S); node, log-prob,
+  // the causal boundary leaf block, the uniforms' base index and (binary
+  // trees) the last Philox block stay in registers
+  const int nitems = kQueryTile * S;
+  int node[kNI], iq[kNI], is[kNI], iblk[kNI];
+  uint32_t rleaf[kNI];  // replay: the given leaf block of each item
+  int64_t ubase[kNI];
+  float acc[kNI];
+  constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
+  RngCache rc[kNC];
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    node[k] = 0;
+    acc[k] = 0.f;
+    iq[k] = it < nitems ? it / S : kQueryTile;
+    is[k] = it < nitems ? it - iq[k] * S : 0;
+    if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
+    const int l = l0 + min(iq[k], nq - 1);
+    iblk[k] = (l + a.coff) / G.LB;
+    ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
+    rleaf[k] = 0u;
+    if (kReplay && iq[k] < kQueryTile)
+      rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * S + is[k]) * a.nbytes, a.nbits, a.nbytes);
+  }
+#pragma unroll
+  for (int k = 0; k < kNC; ++k) {
+    rc[k].ctr = ~0ull;
+    rc[k].w0 = rc[k].w1 = rc[k].w2 = rc[k].w3 = 0u;
+  }
+
+  // pass p < nbatch: causal boundary batch p; then level d, chunk c0
+  LogitPipe<E, D, kLo> pipe;
+  pipe.rmax = ps.base + rows - 1;
+  auto tiles_of = [&](int p, int d, int c0) {
+    if (p < nbatch) return min(kLevelCols / 16, ps.nbt - p * (kLevelCols / 16));
+    return (min(kLevelCols, ps.level_cols(d) - c0) + 15) >> 4;
+  };
+  auto prefetch = [&](int p, int d, int c0) {
+    if (p < nbatch) {
+      const int t0 = p * (kLevelCols / 16);
+      pipe.prefetch(hi, lo, [&](int t) { return ps.brow(t0 + t); }, tiles_of(p, d, c0), lane, w);
+    } else {
+      const int64_t r0 = ps.base + G.off[d + 1] + c0;
+      pipe.prefetch(hi, lo, [&](int t) { return r0 + 16 * t; }, tiles_of(p, d, c0), lane, w);
+    }
+  };
+  int p = 0, d = 0, c0 = 0;  // current pass
+  if (T > 0) prefetch(0, 0, 0);
+  while (p < nbatch || d < T) {
+    const int nt = tiles_of(p, d, c0);
+    if (p < nbatch) {
+      const int t0 = p * (kLevelCols / 16);
+      pipe.run(qa, Xs, hi, lo, [&](int t) { return ps.brow(t0 + t); }, nt, lane, w);
+    } else {
+      const int64_t r0 = ps.base + G.off[d + 1] + c0;
+      pipe.run(qa, Xs, hi, lo, [&](int t) { return r0 + 16 * t; }, nt, lane, w);
+    }
+    __syncthreads();
+    // next pass, and its first tile in flight while this one is consumed
+    int np = p + 1, nd = d, nc0 = c0;
+    if (p >= nbatch) {
+      nc0 = c0 + kLevelCols;
+      if (nc0 >= ps.level_cols(d)) {
+        nc0 = 0;
+        ++nd;
+      }
+    }
+    if (np < nbatch || nd < T) prefetch(np, nd, nc0);
+
+    if (p < nbatch) {
+      // boundary child logits of this batch's depths
+      if (tid < nq) {
+        const int blk = (l0 + tid + a.coff) / G.LB;
+        int t0 = 0;
+        for (int dd = 0; dd < T; ++dd) {
+          // column of the query's boundary node's first child in the global tile space
+          const int gc = 16 * t0 + ((blk >> (lb * (T - dd))) << lb) - ps.bc0(dd) - p * kLevelCols;
+          if (gc >= 0 && gc < kLevelCols)
+            for (int j = 0; j < b; ++j) xb[tid * T * b + dd * b + j] = clampf(Xs[tid * kXS + gc + j], a.maxhalf);
+          t0 += ps.btiles(dd);
+        }
+      }
+      if (p + 1 == nbatch) {
+        // Causal: allowed log-mass of each boundary-path node, bottom-up:
+        // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.
+        __syncthreads();
+        if (tid < nq) {
+          const int blk = (l0 + tid + a.coff) / G.LB;
+          float* la = logA + tid * (T + 1);
+          la[T] = 0.f;
+          for (int dd = T - 1; dd >= 0; --dd) {
+            const int js = (blk >> (lb * (T - 1 - dd))) & (b - 1);
+            const float* xs = xb + tid * T * b + dd * b;
+            float mx = -__builtin_inff();
+            for (int j = 0; j < b; ++j) mx = fmaxf(mx, xs[j]);
+            float se = 0.f;
+            for (int j = 0; j < b; ++j) se += expf(xs[j] - mx);
+            const float lse = mx + logf(se);
+            // terms: logp_j (j < js), logp_js + logA_{d+1}
+            float tm = -__builtin_inff();
+            for (int j = 0; j <= js; ++j) tm = fmaxf(tm, xs[j] - lse + (j == js ? la[dd + 1] : 0.f));
+            float ts = 0.f;
+            for (int j = 0; j <= js; ++j) ts += expf(xs[j] - lse + (j == js ? la[dd + 1] : 0.f) - tm);
+            la[dd] = tm + logf(ts);
+          }
+        }
+      }
+    } else {
+      const int ncols = min(kLevelCols, ps.level_cols(d) - c0);
+      const int shb = lb * (T - d), shc = lb * (T - 1 - d);
+#pragma unroll
+      for (int k = 0; k < kNI; ++k) {
+        const int qi = iq[k];
+        if (qi >= kQueryTile) continue;
+        const int base = (node[k] << lb) - c0;
+        if (base < 0 || base >= ncols) continue;
+        const float* xr = Xs + qi * kXS + base;
+        // log-sum-exp of the clamped child logits
+        float lse;
+        float x[kB ? kB : 1];
+        if constexpr (kB != 0) {
+          float mx = -__builtin_inff();
+#pragma unroll
+          for (int j = 0; j < kB; ++j) {
+            x[j] = clampf(xr[j], a.maxhalf);
+            mx = fmaxf(mx, x[j]);
+          }
+          float se = 0.f;
+#pragma unroll
+          for (int j = 0; j < kB; ++j) se += fast_exp2((x[j] - mx) * kLog2e);
+          lse = mx + fast_log2(se) * kLn2;
+        } else {
+          float mx = -__builtin_inff();
+          for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
+          float se = 0.f;
+          for (int j = 0; j < b; ++j) se += fast_exp2((clampf(xr[j], a.maxhalf) - mx) * kLog2e);
+          lse = mx + fast_log2(se) * kLn2;
+        }
+        if constexpr (kReplay) {  // the given digit, its log-prob (non-causal)
+          const int jr = (int)((rleaf[k] >> (lb * (T - 1 - d))) & (uint32_t)(b - 1));
+          float xj = 0.f;
+          if constexpr (kB != 0) {
+#pragma unroll
+            for (int j = 0; j < kB; ++j)
+              if (j == jr) xj = x[j];
+          } else {
+            xj = clampf(xr[jr], a.maxhalf);
+          }
+          node[k] = (node[k] << lb) + jr;
+          acc[k] += xj - lse;
+          continue;
+        }
+        bool onb = false;
+        int js = 0;
+        float la_d = 0.f, la_c = 0.f;
+        if (a.causal && (iblk[k] >> shb) == node[k]) {
+          onb = true;
+          js = (iblk[k] >> shc) & (b - 1);
+          la_d = logA[qi * (T + 1) + d];
+          la_c = logA[qi * (T + 1) + d + 1];
+        }
+        const int64_t ub = ubase[k] + d * b;
+        RngCache local;
+        local.ctr = ~0ull;
+        local.w0 = local.w1 = local.w2 = local.w3 = 0u;
+        RngCache& cache = kB == 2 ? rc[kB == 2 ? k : 0] : local;
+        float best = -__builtin_inff(), bl = 0.f;
+        int bj = 0;
+        auto consider = [&](int j, float xj) {
+          float lp = xj - lse;
+          if (onb) {
+            if (j < js) lp -= la_d;
+            else if (j == js) lp += la_c - la_d;
+            else lp = -__builtin_inff();
+          }
+          const float u = uniform_at(a.U, a.seed, ub + j, cache);
+          // lp + g up to the common constant -log(ln 2): g = -ln(ln2 * -log2 u)
+          const float sc = lp - kLn2 * fast_log2(-fast_log2(u));
+          if (sc > best) {
+            best = sc;
+            bj = j;
+            bl = lp;
+          }
+        };
+        if constexpr (kB != 0) {
+#pragma unroll
+          for (int j = 0; j < kB; ++j) consider(j, x[j]);
+        } else {
+          for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
+        }
+        node[k] = (node[k] << lb) + bj;
+        acc[k] += bl;
+      }
+    }
+    __syncthreads();
+    p = np;
+    d = nd;
+    c0 = nc0;
+  }
+
+  // weights (softmax over the query's samples) and distinct leaf blocks
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    if (it < nitems) {
+      lf[it] = node[k];
+      lps[it] = acc[k];
+    }
+  }
+  __syncthreads();
+  float wgt[kNI];
+  bool first[kNI];
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    wgt[k] = 0.f;
+    first[k] = false;
+    const int qi = iq[k];
+    if (qi >= kQueryTile) continue;
+    const int s = is[k];
+    const int* lq = lf + qi * S;
+    const float* pq = lps + qi * S;
+    float m = -__builtin_inff();
+    for (int j = 0; j < S; ++j) m = fmaxf(m, pq[j]);
+    float sum = 0.f, tot = 0.f;
+    bool fst = true;
+    for (int j = 0; j < S; ++j) {
+      const float e = fast_exp2((pq[j] - m) * kLog2e);
+      sum += e;
+      if (lq[j] == node[k]) {
+        if (j < s) fst = false;
+        else tot += e;
+      }
+    }
+    const float inv = 1.f / sum;
+    wgt[k] = fast_exp2((acc[k] - m) * kLog2e) * inv;
+    first[k] = fst;
+    acc[k] = tot * inv;  // summed weight of this leaf block (used if first)
+  }
+  // distinct-leaf keys: the leaf for a first occurrence, else INT_MAX
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int it = tid + 256 * k;
+    if (iq[k] < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
+    else if (it < nitems) fl[it] = 0x7fffffff;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kNI; ++k) {
+    const int qi = iq[k];
+    if (qi >= kQueryTile) continue;
+    const int s = is[k];
+    const int l = l0 + qi;
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+    a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = wgt[k];
+    a.leaf[qh * S + s] = node[k];
+    const int* fq = fl + qi * S;
+    if (first[k]) {
+      int rank = 0;
+      for (int j = 0; j < S; ++j) rank += fq[j] < node[k];
+      a.slot_leaf[qh * S + rank] = node[k];
+      a.slot_weight[qh * S + rank] = acc[k];
+    }
+    if (s == 0) {
+      int cnt = 0;
+      for (int j = 0; j < S; ++j) cnt += fq[j] != 0x7fffffff;
+      a.slot_count[qh] = cnt;
+    }
+  }
+}
+
+// Xs (which the final phase's three [64][S] arrays alias: 3 * 64 * 64 * 4
+// bytes < sizeof Xs), logA and the boundary child logits.
+static inline int sample_smem(const Plan& P) {
+  const int T = P.geo.T, b = P.geo.b;
+  return kQueryTile * kXS * 4 + kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
+}
+
+template <bool kReplay, typename E, int D, int kB, int kNI>
+static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
+                              char* rec, hipStream_t st, const uint8_t* paths) {
+  SampleArgs a;
+  a.geo = P.geo;
+  a.B = (int)P.B;
+  a.paths = paths;
+  a.nbits = P.geo.T * P.geo.lb;
+  a.nbytes = (a.nbits + 7) / 8;
+  a.L = (int)P.L;
+  a.H = (int)P.H;
+  a.S = (int)P.S;
+  a.causal = P.p.causal == TA_CAUSAL_EXACT;
+  a.coff = (int)(P.N - P.L);
+  a.maxhalf = 0.5f * P.p.max_logit;
+  a.q = q;
+  a.qsb = P.p.q_strides[0];
+  a.qsl = P.p.q_strides[1];
+  a.qsh = P.p.q_strides[2];
+  a.sum32 = (const float*)(rec + P.rec.summaries);
+  a.sum_hi = rec + P.rec.sum_hi;
+  a.sum_lo = rec + P.rec.sum_lo;
+  a.U = U;
+  a.seed = seed;
+  a.weights = weights;
+  a.wsb = P.p.w_strides[0];
+  a.wsl = P.p.w_strides[1];
+  a.wsh = P.p.w_strides[2];
+  a.leaf = (int*)(rec + P.rec.leaf);
+  a.slot_leaf = (int*)(rec + P.rec.slot_leaf);
+  a.slot_weight = (float*)(rec + P.rec.slot_weight);
+  a.slot_count = (int*)(rec + P.rec.slot_count);
+  const int smem = sample_smem(P);
+  auto launch = [&](auto kern) -> hipError_t {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH), dim3(256), smem, st, a);
+    return hipGetLastError();
+  };
+  return launch(sample_kernel<E, D, kB, kNI, kReplay>);
+}
+
+template <bool kReplay, typename E, int D>
+static hipError_t sample_b(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
+                           hipStream_t st, const uint8_t* pa) {
+  static_assert(kMaxSamples * kQueryTile / 256 == 16, "items per thread");
+  const bool few = P.S <= 16;  // 64 * S / 256 <= 4 items per thread
+  switch (P.geo.b) {
+    case 2: return few ? sample_impl<kReplay, E, D, 2, 4>(P, q, U, seed, w, rec, st, pa)
+                       : sample_impl<kReplay, E, D, 2, 16>(P, q, U, seed, w, rec, st, pa);
+    case 4: return few ? sample_impl<kReplay, E, D, 4, 4>(P, q, U, seed, w, rec, st, pa)
+                       : sample_impl<kReplay, E, D, 4, 16>(P, q, U, seed, w, rec, st, pa);
+    default: return few ? sample_impl<kReplay, E, D, 0, 4>(P, q, U, seed, w, rec, st, pa)
+                        : sample_impl<kReplay, E, D, 0, 16>(P, q, U, seed, w, rec, st, pa);
+  }
+}
+
+template <bool kReplay, typename E>
+static hipError_t sample_d(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
+                           hipStream_t st, const uint8_t* pa) {
+  switch (P.D) {
+    case 32: return sample_b<kReplay, E, 32>(P, q, U, seed, w, rec, st, pa);
+    case 64: return sample_b<kReplay, E, 64>(P, q, U, seed, w, rec, st, pa);
+    case 96: return sample_b<kReplay, E, 96>(P, q, U, seed, w, rec, st, pa);
+    default: return sample_b<kReplay, E, 128>(P, q, U, seed, w, rec, st, pa);
+  }
+}
+
+// The sampler for every supported element type, head dim and branching, with
+// Gumbel-max decisions (kReplay false) or replayed paths (kReplay true).
+template <bool kReplay>
+static hipError_t sample_dispatch(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
+                                  char* rec, hipStream_t st, const uint8_t* paths) {
+  switch (P.p.dtype) {
+    case TA_F32: return sample_d<kReplay, float>(P, q, U, seed, weights, rec, st, paths);
+    case TA_BF16: return sample_d<kReplay, bf16>(P, q, U, seed, weights, rec, st, paths);
+    default: return sample_d<kReplay, f16>(P, q, U, seed, weights, rec, st, paths);
+  }
+}
+
+}  // namespace ta
