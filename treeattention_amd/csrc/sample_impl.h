@@ -165,6 +165,54 @@ __device__ __forceinline__ float uniform_at(const float* U, uint64_t seed, int64
   return word_to_uniform(wi == 0 ? rc.w0 : wi == 1 ? rc.w1 : wi == 2 ? rc.w2 : rc.w3);
 }
 
+// Lane (i - R) mod 16 of the same 16-lane row: a DPP row_ror.
+template <int R>
+__device__ __forceinline__ int row_ror(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, 0x120 + R, 0xf, 0xf, false);
+}
+template <int R>
+__device__ __forceinline__ float row_ror(float x) {
+  return __int_as_float(row_ror<R>(__float_as_int(x)));
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, row_ror<8>(x));
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<2>(x));
+  return fmaxf(x, row_ror<1>(x));
+}
+__device__ __forceinline__ float row_sum16(float x) {
+  x += row_ror<8>(x);
+  x += row_ror<4>(x);
+  x += row_ror<2>(x);
+  return x + row_ror<1>(x);
+}
+// Over the other lanes j of the row (j = s - R mod 16, earlier than s when
+// R <= s): fst is cleared if an earlier lane holds the same leaf, and tot
+// adds e of the later lanes with the same leaf.
+template <int R = 1>
+__device__ __forceinline__ void row_dups16(int n, float e, int s, float& tot, bool& fst) {
+  if constexpr (R < 16) {
+    const int nr = row_ror<R>(n);
+    const float er = row_ror<R>(e);
+    if (nr == n) {
+      if (R <= s) fst = false;
+      else tot += er;
+    }
+    row_dups16<R + 1>(n, e, s, tot, fst);
+  }
+}
+// rank = number of row keys below n; cnt = number of row keys that are not
+// INT_MAX (this lane's included).
+template <int R = 0>
+__device__ __forceinline__ void row_rank16(int key, int n, int& rank, int& cnt) {
+  if constexpr (R < 16) {
+    const int kr = R == 0 ? key : row_ror<R>(key);
+    rank += kr < n;
+    cnt += kr != 0x7fffffff;
+    row_rank16<R + 1>(key, n, rank, cnt);
+  }
+}
+
 // kB: branching known at compile time (2 or 4), or 0 for the runtime value.
 // kNI: (query, sample) items per thread, >= 64 * S / 256.
 // kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
@@ -284,40 +332,59 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     if (np < nbatch || nd < T) prefetch(np, nd, nc0);
 
     if (p < nbatch) {
-      // boundary child logits of this batch's depths
-      if (tid < nq) {
-        const int blk = (l0 + tid + a.coff) / G.LB;
+      // boundary child logits of this batch's depths: query tid & 63, depths
+      // w, w + 4, ... (all four waves)
+      const int qb = tid & 63;
+      if (qb < nq) {
+        const int blk = (l0 + qb + a.coff) / G.LB;
         int t0 = 0;
         for (int dd = 0; dd < T; ++dd) {
           // column of the query's boundary node's first child in the global tile space
           const int gc = 16 * t0 + ((blk >> (lb * (T - dd))) << lb) - ps.bc0(dd) - p * kLevelCols;
-          if (gc >= 0 && gc < kLevelCols)
-            for (int j = 0; j < b; ++j) xb[tid * T * b + dd * b + j] = clampf(Xs[tid * kXS + gc + j], a.maxhalf);
+          if ((dd & 3) == w && gc >= 0 && gc < kLevelCols)
+            for (int j = 0; j < b; ++j) xb[qb * T * b + dd * b + j] = clampf(Xs[qb * kXS + gc + j], a.maxhalf);
           t0 += ps.btiles(dd);
         }
       }
       if (p + 1 == nbatch) {
         // Causal: allowed log-mass of each boundary-path node, bottom-up:
-        // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.
+        // A_T = 1, A_d = sum_{j<j*} p_j + p_{j*} A_{d+1}.  Per depth (waves
+        // split the depths), in log2 units: lt = log2 sum_{j<j*} p_j and
+        // lj = log2 p_{j*}, written over the depth's first two logits.
+        __syncthreads();
+        if (qb < nq) {
+          const int blk = (l0 + qb + a.coff) / G.LB;
+          for (int dd = w; dd < T; dd += 4) {
+            const int js = (blk >> (lb * (T - 1 - dd))) & (b - 1);
+            float* xs = xb + qb * T * b + dd * b;
+            float mx = -__builtin_inff(), ml = -__builtin_inff();
+            for (int j = 0; j < b; ++j) {
+              mx = fmaxf(mx, xs[j]);
+              if (j < js) ml = fmaxf(ml, xs[j]);
+            }
+            float se = 0.f, sl = 0.f;
+            for (int j = 0; j < b; ++j) {
+              se += fast_exp2((xs[j] - mx) * kLog2e);
+              if (j < js) sl += fast_exp2((xs[j] - ml) * kLog2e);
+            }
+            const float l2se = fast_log2(se);
+            const float lj = (xs[js] - mx) * kLog2e - l2se;
+            const float lt = js > 0 ? (ml - mx) * kLog2e + fast_log2(sl) - l2se : -__builtin_inff();
+            xs[0] = lt;
+            xs[1] = lj;
+          }
+        }
         __syncthreads();
         if (tid < nq) {
-          const int blk = (l0 + tid + a.coff) / G.LB;
           float* la = logA + tid * (T + 1);
+          const float* xq = xb + tid * T * b;
+          float c = 0.f;  // log2 A_{d+1}
           la[T] = 0.f;
           for (int dd = T - 1; dd >= 0; --dd) {
-            const int js = (blk >> (lb * (T - 1 - dd))) & (b - 1);
-            const float* xs = xb + tid * T * b + dd * b;
-            float mx = -__builtin_inff();
-            for (int j = 0; j < b; ++j) mx = fmaxf(mx, xs[j]);
-            float se = 0.f;
-            for (int j = 0; j < b; ++j) se += expf(xs[j] - mx);
-            const float lse = mx + logf(se);
-            // terms: logp_j (j < js), logp_js + logA_{d+1}
-            float tm = -__builtin_inff();
-            for (int j = 0; j <= js; ++j) tm = fmaxf(tm, xs[j] - lse + (j == js ? la[dd + 1] : 0.f));
-            float ts = 0.f;
-            for (int j = 0; j <= js; ++j) ts += expf(xs[j] - lse + (j == js ? la[dd + 1] : 0.f) - tm);
-            la[dd] = tm + logf(ts);
+            const float lt = xq[dd * b], v = xq[dd * b + 1] + c;
+            const float hi = fmaxf(lt, v), lo = fminf(lt, v);
+            c = hi + fast_log2(1.f + fast_exp2(lo - hi));
+            la[dd] = c * kLn2;
           }
         }
       }
@@ -333,7 +400,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
         const float* xr = Xs + qi * kXS + base;
         // log-sum-exp of the clamped child logits
         float lse;
-        float x[kB ? kB : 1];
+        float x[kB ? kB : 1], ex[kB ? kB : 1];
         if constexpr (kB != 0) {
           float mx = -__builtin_inff();
 #pragma unroll
@@ -343,7 +410,10 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
           }
           float se = 0.f;
 #pragma unroll
-          for (int j = 0; j < kB; ++j) se += fast_exp2((x[j] - mx) * kLog2e);
+          for (int j = 0; j < kB; ++j) {
+            ex[j] = fast_exp2((x[j] - mx) * kLog2e);
+            se += ex[j];
+          }
           lse = mx + fast_log2(se) * kLn2;
         } else {
           float mx = -__builtin_inff();
@@ -376,10 +446,64 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
           la_c = logA[qi * (T + 1) + d + 1];
         }
         const int64_t ub = ubase[k] + d * b;
+        if constexpr (kB != 0) {
+          // Gumbel-max in ratio form: lp_j - ln(-ln u_j) is, up to constants
+          // common to all children, ln(p_j / E_j) with E_j = -log2 u_j > 0,
+          // so the argmax is that of ex_j / E_j (ex_j = 2^((x_j - max) log2 e),
+          // proportional to p_j); on the boundary the allowed weights are
+          // ex_j (j < j*) and ex_j* A_{d+1}, rescaled to their own maximum.
+          float u[kB];
+          if constexpr (kB == 4) {  // the decision's four uniforms are one Philox block
+            if (a.U) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) u[j] = a.U[ub + j];
+            } else {
+              const Philox4 ph = philox4x32_10((uint64_t)ub >> 2, a.seed);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) u[j] = word_to_uniform(ph.w[j]);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < kB; ++j) u[j] = uniform_at(a.U, a.seed, ub + j, rc[kB == 2 ? k : 0]);
+          }
+          float wj[kB];
+#pragma unroll
+          for (int j = 0; j < kB; ++j) wj[j] = ex[j];
+          if (onb) {
+            float y[kB], my = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < kB; ++j) {
+              y[j] = j < js ? x[j] * kLog2e : j == js ? x[j] * kLog2e + la_c * kLog2e : -__builtin_inff();
+              my = fmaxf(my, y[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < kB; ++j) wj[j] = j <= js ? fast_exp2(y[j] - my) : 0.f;
+          }
+          float bw = wj[0], be = -fast_log2(u[0]);
+          int bj = 0;
+#pragma unroll
+          for (int j = 1; j < kB; ++j) {
+            const float e = -fast_log2(u[j]);
+            if (wj[j] * be > bw * e) {
+              bw = wj[j];
+              be = e;
+              bj = j;
+            }
+          }
+          float xb_ = x[0];
+#pragma unroll
+          for (int j = 1; j < kB; ++j)
+            if (j == bj) xb_ = x[j];
+          float lp = xb_ - lse;
+          if (onb) lp += bj < js ? -la_d : la_c - la_d;
+          node[k] = (node[k] << lb) + bj;
+          acc[k] += lp;
+          continue;
+        }
         RngCache local;
         local.ctr = ~0ull;
         local.w0 = local.w1 = local.w2 = local.w3 = 0u;
-        RngCache& cache = kB == 2 ? rc[kB == 2 ? k : 0] : local;
+        RngCache& cache = local;
         float best = -__builtin_inff(), bl = 0.f;
         int bj = 0;
         auto consider = [&](int j, float xj) {
@@ -398,12 +522,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
             bl = lp;
           }
         };
-        if constexpr (kB != 0) {
-#pragma unroll
-          for (int j = 0; j < kB; ++j) consider(j, x[j]);
-        } else {
-          for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
-        }
+        for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
         node[k] = (node[k] << lb) + bj;
         acc[k] += bl;
       }
@@ -415,6 +534,33 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   }
 
   // weights (softmax over the query's samples) and distinct leaf blocks
+  if (S == 16) {
+    // item tid + 256 k: a query's 16 samples are the 16 lanes of one DPP row
+    const int s = lane & 15;
+#pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      const float m = row_max16(acc[k]);
+      const float e = fast_exp2((acc[k] - m) * kLog2e);
+      const float inv = 1.f / row_sum16(e);
+      float tot = e;  // weight of this leaf block summed over the samples from s on
+      bool fst = true;
+      row_dups16(node[k], e, s, tot, fst);
+      int rank = 0, cnt = 0;
+      row_rank16(fst ? node[k] : 0x7fffffff, node[k], rank, cnt);
+      const int qi = iq[k];
+      if (qi >= kQueryTile) continue;
+      const int l = l0 + qi;
+      const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+      a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = e * inv;
+      a.leaf[qh * S + s] = node[k];
+      if (fst) {
+        a.slot_leaf[qh * S + rank] = node[k];
+        a.slot_weight[qh * S + rank] = tot * inv;
+      }
+      if (s == 0) a.slot_count[qh] = cnt;
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < kNI; ++k) {
     const int it = tid + 256 * k;
