@@ -157,6 +157,13 @@ def test_fp32_causal_natural_b4():
     run_case(1, 256, 2, 64, 8, 4, 16, "natural", True, torch.float32)
 
 
+def test_causal_level_wider_than_one_chunk():
+    # 256 leaf blocks: the deepest level spans two 128-column chunks of the
+    # tree-gradient kernel, and the second is out of causal reach for the
+    # first half of the query tiles (its products are skipped)
+    run_case(1, 4096, 1, 32, 4, 2, 16, "natural", True, torch.bfloat16)
+
+
 def test_seed_path_equals_explicit_uniforms_and_is_deterministic():
     from treeattention_amd.function import TreeOptions, record_views, tree_backward, tree_forward
 

@@ -420,7 +420,17 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   constexpr int KT = kChunk / M::K;  // k-steps of the C^T G^T product per chunk
   F af[2][KS];
   F at[NMD][KT];
-  auto kcols_of = [&](int d, int c0) { return (min(kChunk, G.pw[d + 1] - c0) + 31) / 32 * 32; };
+  // Exact causal restriction: every sampled block is <= blk_hi, so only
+  // children of depth-d nodes over those blocks hold G entries for this tile;
+  // the products skip the other columns, whose G^T rows are still written as
+  // zeros.  (The reference causal mode samples past the query's position.)
+  const bool cz = a.causal;
+  const int blk_hi = (l0 + nq - 1 + (a.N - a.L)) / G.LB;
+  auto reach = [&](int d) {
+    const int n = G.pw[d + 1];
+    return cz ? min(n, ((blk_hi >> (G.lb * (T - d))) + 1) << G.lb) : n;
+  };
+  auto kcols_of = [&](int d, int c0) { return (max(0, min(kChunk, reach(d) - c0)) + 31) / 32 * 32; };
   auto load_af = [&](int d, int c0) {
     const int64_t r0 = (int64_t)bh * rows + G.off[d + 1] + c0;
     const int kc = kcols_of(d, c0);
@@ -456,6 +466,8 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     const int lam = d + 1, lvl = G.pw[lam];
     const int ncols = min(kChunk, lvl - c0);
     const int kcols = (ncols + 31) / 32 * 32;  // inside the level's zero padding
+    const int rcols = max(0, min(ncols, reach(d) - c0));  // columns that can be nonzero
+    const int rk = (rcols + 31) / 32 * 32;
     int nd = d, nc0 = c0 + kChunk;
     if (nc0 >= lvl) {
       nc0 = 0;
@@ -465,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ct = w + 4 * j;
-      if (ct < kcols / 16) {
+      if (ct < rk / 16) {
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) {
           f32x4 c = zero4();
@@ -489,7 +501,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       z8(sm.Gm + r * kGS + cc);
     }
     __syncthreads();
-    build_g_p<E, kP, kB>(G, d, c0, ncols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    if (rcols > 0) build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
     __syncthreads();
     if (a.refc) {
       // boundary-mass gradient of the reference causal mode (ref_causal_grad_kernel)
@@ -525,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     // dq^T += C^T G^T: A = C^T rows (head dims, registers), B = G rows (LDS)
 #pragma unroll
     for (int ks = 0; ks < KT; ++ks) {
-      if (ks < kcols / M::K) {
+      if (ks < rk / M::K) {
         F bg[4];
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) bg[qt] = ld_frag(sm.Gm + (16 * qt + col) * kGS + ks * M::K + M::KPL * g);
