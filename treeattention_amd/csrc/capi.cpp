@@ -116,11 +116,11 @@ int make_plan(const ta_problem* p, Plan* P) {
     return fail(TA_ERR_UNSUPPORTED, "too many leaf blocks x query chunks for the bucket table (NL=%lld)",
                 (long long)NL);
   // summary gradient: chunks of 384 summary rows; queries split into blocks of
-  // 32 so the product has about 512 workgroups (two per CU)
+  // 64 so the product has about 512 workgroups (two per CU)
   const int64_t qtiles = (L + kQueryTile - 1) / kQueryTile;
   P->Lp = qtiles * kQueryTile;
   const int64_t rowchunks = (G.NS / 16 + 23) / 24;
-  const int64_t kblocks = P->Lp / 32;
+  const int64_t kblocks = P->Lp / 64;
   int64_t qsplit = (512 + rowchunks * P->BH - 1) / (rowchunks * P->BH);
   if (qsplit < 1) qsplit = 1;
   if (qsplit > kblocks) qsplit = kblocks;

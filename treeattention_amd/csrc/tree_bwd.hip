@@ -600,7 +600,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
 // global loads are in flight while the current one is multiplied) and every
 // G^T row is read once, straight from global memory into MFMA fragments.
 constexpr int kDcRows = 3;   // row tiles per wave
-constexpr int kDcKB = 32;    // queries per staged block
+constexpr int kDcKB = 64;    // queries per staged block (whole 128-byte lines of G^T rows)
 
 template <typename E, int D>
 __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
