@@ -157,6 +157,14 @@ def test_fp32_causal_natural_b4():
     run_case(1, 256, 2, 64, 8, 4, 16, "natural", True, torch.float32)
 
 
+@pytest.mark.parametrize("b,L,LB,causal", [(2, 8192, 16, False), (4, 4096, 4, True)])
+def test_levels_wider_than_one_sampler_pass(b, L, LB, causal):
+    # 512 / 1024 leaf blocks: the deepest levels take two / four passes of the
+    # sampler's 256-column logit tile, so an item that moved in one pass must
+    # not decide again in a later pass of the same level
+    run_case(1, L, 1, 32, 4, b, LB, "natural", causal, torch.bfloat16)
+
+
 def test_causal_level_wider_than_one_chunk():
     # 256 leaf blocks: the deepest level spans two 128-column chunks of the
     # tree-gradient kernel, and the second is out of causal reach for the
@@ -185,40 +193,74 @@ def test_seed_path_equals_explicit_uniforms_and_is_deterministic():
         assert torch.equal(a, c)
 
 
-def test_op_level_hierarchical_attention_matches_reference_restatement():
-    """Reference op signature (L,B,E) with heap node keys, against ``ref_forward_non_causal``."""
+# (L, B, H, D, S) of the reference's own end-to-end parity test
+# (test_harness_smoke.py:824-917); D = 16 runs zero-padded to 32 head dims.
+REFERENCE_E2E_SHAPES = [(8, 1, 2, 16, 4), (32, 2, 2, 16, 4), (64, 1, 8, 16, 4), (128, 1, 2, 64, 8), (512, 2, 4, 32, 8),
+                        (32, 2, 2, 32, 4)]
+
+
+@pytest.mark.parametrize("L,B,H,D,S", REFERENCE_E2E_SHAPES)
+def test_op_level_hierarchical_attention_matches_reference_restatement(L, B, H, D, S):
+    """Reference op signature (L,B,E) with heap node keys, against ``ref_forward_non_causal``:
+    sampled leaves equal wherever every decision's margin exceeds 1e-3; weights, output and
+    gradients against the restatement on the GPU's own paths (returned packed, the reference's
+    record format)."""
     import treeattention_amd as ta
 
-    L, B, H, D, S = 32, 2, 2, 32, 4
+    print(f"[case] op-level L={L} B={B} H={H} D={D} S={S}", flush=True)
     E = H * D
     g = torch.Generator().manual_seed(1234)
     query = torch.randn(L, B, E, generator=g)
     key = torch.randn(L - 1, B, E, generator=g)
     value = torch.randn(L, B, E, generator=g)
     gout = torch.randn(L, B, E, generator=g)
-    T = 5
+    T = int(math.log2(L))
     U = O.uniforms(0, (B, L, H, S, T, 2))
     qd, kd, vd = (x.cuda().requires_grad_(True) for x in (query, key, value))
-    out, w = ta.hierarchical_attention(qd, kd, vd, num_heads=H, num_samples=S, uniforms=torch.from_numpy(U).cuda())
+    out, w, paths = ta.hierarchical_attention(qd, kd, vd, num_heads=H, num_samples=S,
+                                              uniforms=torch.from_numpy(U).cuda(), return_paths=True)
     out.backward(gout.cuda())
     q4 = query.double().numpy().reshape(L, B, H, D)
     k4 = key.double().numpy().reshape(L - 1, B, H, D)
     v4 = value.double().numpy().reshape(L, B, H, D)
-    gum = O.gumbel(U).transpose(1, 0, 2, 3, 4, 5)
-    ref_out, ref_w, ref_idx = O.ref_forward_non_causal(q4, k4, v4, gum)
-    assert rel(f64(out), ref_out.reshape(L, B, E)) < 1e-5
-    assert rel(w.detach().cpu().numpy(), ref_w) < 1e-5
-    # gradients: explicit oracle backward on the node-key tree
     qb, vb = q4.transpose(1, 0, 2, 3), v4.transpose(1, 0, 2, 3)
     C = O.nodekeys_to_summaries(k4.transpose(1, 2, 0, 3))
-    idx = ref_idx.transpose(1, 0, 2, 3)
-    wb = ref_w.transpose(1, 0, 2, 3)
-    dq, dC, _, dv = O.tree_backward(qb, np.zeros_like(vb), vb, C, 2, 1, idx, wb,
+    # paths: the restatement's sampling, compared where no decision is within 1e-3
+    gum = O.gumbel(U).transpose(1, 0, 2, 3, 4, 5)
+    _, _, ref_idx = O.ref_forward_non_causal(q4, k4, v4, gum)
+    _, _, margins = O.tree_sample(qb, C, 2, 1, U, False)
+    leaves = O.unpack_paths(paths.cpu().numpy(), L).transpose(1, 0, 2, 3)  # (B, L, H, S)
+    clean = margins.min(axis=-1) > 1e-3
+    mism = leaves != ref_idx.transpose(1, 0, 2, 3)
+    assert not (mism & clean).any(), f"{int((mism & clean).sum())} clean samples differ"
+    assert clean.mean() > 0.9
+    # weights and output on the GPU's paths
+    wb = O.sample_weights(O.path_logprobs(qb, C, 2, L, leaves))
+    o_s, _ = O.leaf_attention(qb, np.zeros_like(vb), vb, leaves, 1, False, 1.0)
+    out_ref = np.einsum("blhs,blhsd->blhd", wb, o_s)
+    assert rel(f64(out), out_ref.transpose(1, 0, 2, 3).reshape(L, B, E)) < 1e-5
+    assert rel(w.detach().cpu().numpy(), wb.transpose(1, 0, 2, 3)) < 1e-5
+    # gradients: explicit oracle backward on the node-key tree
+    dq, dC, _, dv = O.tree_backward(qb, np.zeros_like(vb), vb, C, 2, 1, leaves, wb,
                                     gout.double().numpy().reshape(L, B, H, D).transpose(1, 0, 2, 3), False)
     dkn = O.nodekeys_adjoint(dC)  # (B,H,K,D)
     assert rel(f64(qd.grad).reshape(L, B, H, D).transpose(1, 0, 2, 3), dq) < 1e-5
     assert rel(f64(kd.grad).reshape(L - 1, B, H, D).transpose(1, 2, 0, 3), dkn) < 1e-5
     assert rel(f64(vd.grad).reshape(L, B, H, D).transpose(1, 0, 2, 3), dv) < 1e-5
+
+
+def test_op_level_block_size_invariance():
+    """The reference streams its sampler over query blocks of ``block_size``; the result does not
+    depend on it (its own block-size test, test_harness_smoke.py:391-421)."""
+    import treeattention_amd as ta
+
+    L, B, H, D, S = 64, 1, 2, 32, 4
+    g = torch.Generator().manual_seed(7)
+    query, key, value = (torch.randn(n, B, H * D, generator=g).cuda() for n in (L, L - 1, L))
+    outs = [ta.hierarchical_attention(query, key, value, num_heads=H, num_samples=S, block_size=bs, seed=3)
+            for bs in (1, 7, 64, 256)]
+    for o, w in outs[1:]:
+        assert torch.equal(o, outs[0][0]) and torch.equal(w, outs[0][1])
 
 
 def test_op_level_edge_cases():

@@ -308,7 +308,12 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
       pipe.prefetch(hi, lo, [&](int t) { return r0 + 16 * t; }, tiles_of(p, d, c0), lane, w);
     }
   };
-  int p = 0, d = 0, c0 = 0;  // current pass
+  // A level wider than kLevelCols children takes several passes, run from the
+  // highest column chunk down: an item that moves in the pass at c0 lands on a
+  // node >= c0 of the next depth, whose children (>= 2 c0) lie past every
+  // later pass of the level, so no item decides twice in one level.
+  auto last_c0 = [&](int dd) { return (ps.level_cols(dd) - 1) / kLevelCols * kLevelCols; };
+  int p = 0, d = 0, c0 = 0;  // current pass (level 0 has b <= kLevelCols children)
   if (T > 0) prefetch(0, 0, 0);
   while (p < nbatch || d < T) {
     const int nt = tiles_of(p, d, c0);
@@ -323,10 +328,11 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     // next pass, and its first tile in flight while this one is consumed
     int np = p + 1, nd = d, nc0 = c0;
     if (p >= nbatch) {
-      nc0 = c0 + kLevelCols;
-      if (nc0 >= ps.level_cols(d)) {
-        nc0 = 0;
+      if (c0 > 0) {
+        nc0 = c0 - kLevelCols;
+      } else {
         ++nd;
+        nc0 = nd < T ? last_c0(nd) : 0;
       }
     }
     if (np < nbatch || nd < T) prefetch(np, nd, nc0);
