@@ -1,0 +1,125 @@
+"""GPU checks at BASELINE.json's full sizes (C2-C5), where the float64 oracle
+cannot run the whole problem:
+
+* parity on a query subset: the last 64 queries of the first and the last
+  (batch, head) -- with bottom-right causal alignment a suffix keeps its
+  positions -- against the oracle with the same in-kernel uniforms (Philox
+  words computed for exactly those samples): sampled leaf blocks equal where
+  every decision's margin exceeds 1e-3, weights, output rows and dq rows
+  within 2e-2 on the GPU's own paths;
+* size-independent identities over the whole problem: weights are a softmax
+  over samples (non-negative, summing to one), every sampled block is
+  reachable (causal), sum_n dv_n = sum_l dout_l per (batch, head) (each
+  sample's leaf softmax and the sample weights sum to one), and
+  sum_n dk_n = 0 per (batch, head) (shifting every key of a head by one vector
+  changes neither a leaf block's softmax nor any node's child softmax).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tree_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# name: B, L, H, D, dtype, branching, leaf block, samples, causal, input kind
+FULL = {
+    "C2": (4, 4096, 16, 64, torch.bfloat16, 2, 64, 8, False, "normal"),
+    "C3": (2, 16384, 16, 128, torch.bfloat16, 4, 64, 16, True, "normal"),
+    "C4": (1, 131072, 8, 128, torch.bfloat16, 2, 128, 16, False, "scaled"),
+    "C5-D32": (8, 8192, 32, 32, torch.float16, 2, 32, 8, True, "skewed"),
+    "C5-D96": (8, 8192, 32, 96, torch.float16, 2, 32, 8, True, "skewed"),
+}
+SUB = 64
+
+
+def inputs(B, L, H, D, dtype, kind):
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q, k, v, do = (torch.randn(B, L, H, D, device="cuda", generator=g) for _ in range(4))
+    if kind == "scaled":
+        q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    elif kind == "skewed":  # Student-t(3) keys, queries with a shared direction x3
+        chi = sum(torch.randn(B, L, H, 1, device="cuda", generator=g) ** 2 for _ in range(3)) / 3
+        k = k / chi.sqrt()
+        u = torch.randn(D, device="cuda", generator=g)
+        q = q + 3 * u / u.norm()
+    return [x.to(dtype) for x in (q, k, v, do)]
+
+
+def uniforms_at(seed: int, flat: np.ndarray) -> np.ndarray:
+    """The generator's uniforms at the given flat indices of the (B, L, H, S, T, b) tensor."""
+    flat = flat.astype(np.uint64)
+    blk = flat >> np.uint64(2)
+    ctr = np.zeros((flat.size, 4), dtype=np.uint32)
+    ctr[:, 0] = (blk & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    ctr[:, 1] = (blk >> np.uint64(32)).astype(np.uint32)
+    key = np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], dtype=np.uint32)
+    words = O.philox4x32_10(ctr, key)[np.arange(flat.size), (flat & np.uint64(3)).astype(np.int64)]
+    return (((words >> np.uint32(8)).astype(np.float64) + 0.5) * 2.0**-24).astype(np.float32)
+
+
+def rel(x, y):
+    return float(np.linalg.norm(x - y) / max(np.linalg.norm(y), 1e-30))
+
+
+@pytest.mark.parametrize("name", sorted(FULL))
+def test_full_size(name):
+    from treeattention_amd.function import TreeOptions, record_views, tree_backward, tree_forward
+
+    B, L, H, D, dtype, b, LB, S, causal, kind = FULL[name]
+    mode = "natural" if b != 2 else "compat"
+    print(f"[case] full size {name}: B={B} L={L} H={H} D={D} {dtype} b={b} LB={LB} S={S} causal={causal}", flush=True)
+    q, k, v, do = inputs(B, L, H, D, dtype, kind)
+    opts = TreeOptions(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, causal=causal, seed=0)
+    out, w, rec = tree_forward(q, k, v, opts)
+    leaves_t, _ = record_views(q, k, v, opts, rec)
+    dq, dk, dv = tree_backward(q, k, v, w, rec, do, opts)
+    torch.cuda.synchronize()
+    NL = L // LB
+    T = round(math.log(NL, b))
+
+    # identities over the whole problem
+    for t in (out, dq, dk, dv):
+        assert torch.isfinite(t.float()).all()
+    assert (w >= 0).all() and (w.sum(-1) - 1).abs().max().item() < 1e-5
+    assert int(leaves_t.min()) >= 0 and int(leaves_t.max()) < NL
+    if causal:
+        blk = (torch.arange(L, device="cuda") // LB).view(1, L, 1, 1)
+        assert (leaves_t <= blk).all()
+    sdv, sdo = dv.float().sum(1), do.float().sum(1)  # (B, H, D)
+    assert rel(sdv.cpu().numpy(), sdo.cpu().numpy()) < 2e-2
+    dkf = dk.float()
+    shift = dkf.sum(1).norm(dim=-1)                                      # |sum_n dk_n| per (b, h)
+    scale_ = dkf.pow(2).sum((1, 3)).sqrt()                               # sqrt(N) * rms row norm
+    assert (shift / scale_).max().item() < 2e-2, (shift / scale_).max().item()
+
+    # parity on the last SUB queries of the first and the last (batch, head)
+    sc = 1.0 / math.sqrt(D)
+    lsub = np.arange(L - SUB, L)
+    for bb, h in ((0, 0), (B - 1, H - 1)):
+        f64 = lambda t: t[bb:bb + 1, :, h:h + 1].float().cpu().numpy().astype(np.float64)
+        kq, vq = f64(k), f64(v)
+        qs, dos = f64(q)[:, -SUB:], f64(do)[:, -SUB:]
+        C = O.summaries(kq, b, LB, mode)
+        s_, t_, j_ = np.meshgrid(np.arange(S), np.arange(T), np.arange(b), indexing="ij")
+        flat = (((((bb * L + lsub[:, None, None, None]) * H + h) * S + s_[None]) * T + t_[None]) * b + j_[None])
+        U = uniforms_at(0, flat.reshape(-1)).reshape(1, SUB, 1, S, T, b)
+        idx_o, _, margins = O.tree_sample(qs, C, b, LB, U, causal, N=L)
+        lv = leaves_t[bb:bb + 1, -SUB:, h:h + 1].cpu().numpy().astype(np.int64)
+        clean = margins.min(axis=-1) > 1e-3
+        assert not ((lv != idx_o) & clean).any(), f"{int(((lv != idx_o) & clean).sum())} clean samples differ"
+        assert clean.mean() > 0.9
+        w_ref = O.sample_weights(O.path_logprobs(qs, C, b, NL, lv))
+        o_s, _ = O.leaf_attention(qs, kq, vq, lv, LB, causal, sc)
+        out_ref = np.einsum("blhs,blhsd->blhd", w_ref, o_s)
+        assert rel(w[bb:bb + 1, -SUB:, h:h + 1].cpu().numpy(), w_ref) < 1e-4
+        assert rel(f64(out)[:, -SUB:], out_ref) < 2e-2
+        dq_o, _, _, _ = O.tree_backward(qs, kq, vq, C, b, LB, lv, w_ref, dos, causal, sc)
+        r = rel(f64(dq)[:, -SUB:], dq_o)
+        print(f"  (b={bb}, h={h}) clean {clean.mean():.3f}, dq rel err {r:.3g}", flush=True)
+        assert r < 2e-2
