@@ -52,13 +52,14 @@ def f64(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", backward=True, scale=None):
+def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", backward=True, scale=None, N=None):
     from treeattention_amd.function import TreeOptions, record_views, tree_backward, tree_forward
 
-    print(f"[case] B={B} L={L} H={H} D={D} S={S} b={b} LB={LB} mode={mode} causal={causal} {dtype} {kind}",
+    N = L if N is None else N
+    print(f"[case] B={B} L={L} N={N} H={H} D={D} S={S} b={b} LB={LB} mode={mode} causal={causal} {dtype} {kind}",
           flush=True)
-    q, k, v, do = make_inputs(B, L, H, D, dtype, seed, kind)
-    nl = L // LB
+    q, k, v, do = make_inputs(B, L, H, D, dtype, seed, kind, N=N)
+    nl = N // LB
     T = O.tree_depth(nl, b)
     U = O.uniforms(seed, (B, L, H, S, T, b))
     dev = torch.device("cuda:0")
@@ -83,13 +84,13 @@ def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", b
         pad += (n + 31) // 32 * 32
 
     # K2: paths against the oracle's own sampling
-    idx_o, lp_o, margins = O.tree_sample(q64, C, b, LB, U, causal)
+    idx_o, lp_o, margins = O.tree_sample(q64, C, b, LB, U, causal, N=N)
     clean = margins.min(axis=-1) > 1e-3
     mism = (leaves != idx_o)
     assert not (mism & clean).any(), f"{int((mism & clean).sum())} clean samples differ"
     assert clean.mean() > 0.9
     if causal:
-        blk = (np.arange(L) // LB)[None, :, None, None]
+        blk = ((np.arange(L) + N - L) // LB)[None, :, None, None]
         assert (leaves <= blk).all()
 
     # K2 weights + K3 output, oracle on the GPU's paths
@@ -105,7 +106,7 @@ def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", b
     if backward:
         dq, dk, dv = tree_backward(qg, kg, vg, w, rec, dog, opts)
         dq_o, dC, dk_leaf, dv_o = O.tree_backward(q64, k64, v64, C, b, LB, leaves, w_ref, do64, causal, sc)
-        dk_o = dk_leaf + O.pool_adjoint(dC, L, b, LB, mode)
+        dk_o = dk_leaf + O.pool_adjoint(dC, N, b, LB, mode)
         for name, got, ref in (("dq", dq, dq_o), ("dk", dk, dk_o), ("dv", dv, dv_o)):
             r = rel(f64(got), ref)
             print(f"  {name} rel err {r:.3g}", flush=True)
@@ -163,6 +164,35 @@ def test_levels_wider_than_one_sampler_pass(b, L, LB, causal):
     # sampler's 256-column logit tile, so an item that moved in one pass must
     # not decide again in a later pass of the same level
     run_case(1, L, 1, 32, 4, b, LB, "natural", causal, torch.bfloat16)
+
+
+@pytest.mark.parametrize("S,b,LB,L,D,causal,dtype", [(32, 4, 16, 1024, 64, True, torch.bfloat16),
+                                                     (64, 2, 8, 512, 32, False, torch.float32)])
+def test_more_than_sixteen_samples(S, b, LB, L, D, causal, dtype):
+    # 16 (query, sample) items per sampler thread and 64-lane groups per query
+    # in the tree-gradient scans
+    run_case(1, L, 2, D, S, b, LB, "natural", causal, dtype)
+
+
+@pytest.mark.parametrize("b,LB,L,causal", [(8, 1, 512, False), (16, 16, 4096, True)])
+def test_branching_eight_and_sixteen(b, LB, L, causal):
+    # branching outside {2, 4}: the runtime-b sampler and tree-gradient paths
+    run_case(1, L, 2, 64, 8, b, LB, "natural", causal, torch.bfloat16)
+
+
+@pytest.mark.parametrize("b,LB,L,D,causal,dtype", [(2, 7, 112, 96, True, torch.bfloat16),
+                                                   (4, 3, 192, 64, False, torch.bfloat16),
+                                                   (2, 48, 384, 128, True, torch.float16)])
+def test_odd_leaf_blocks_and_partial_query_tiles(b, LB, L, D, causal, dtype):
+    # leaf blocks that are not a power of two (padded key tiles), L not a
+    # multiple of the 64-query tile
+    run_case(2, L, 2, D, 8, b, LB, "natural", causal, dtype)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fewer_queries_than_keys(causal):
+    # L = 256 queries over N = 1024 keys (causal: bottom-right aligned)
+    run_case(1, 256, 2, 64, 8, 2, 16, "compat", causal, torch.bfloat16, N=1024)
 
 
 def test_causal_level_wider_than_one_chunk():
