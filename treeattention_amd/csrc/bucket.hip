@@ -85,6 +85,33 @@ __global__ __launch_bounds__(kQueryChunk) void bucket_pass_kernel(BucketArgs a) 
   }
 }
 
+constexpr int kScanBatch = 16;  // counts loaded per batch by one scan thread
+
+// Exclusive prefix of v over the 1024 threads of the workgroup (and the
+// total): a shuffle scan inside each wave, then over the 16 wave totals.
+// part must hold 16 ints; every thread calls it.
+__device__ __forceinline__ int block_scan_1024(int v, int* part, int tid, int& total) {
+  const int lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();  // part[] is free (an earlier scan's readers are done)
+  if (lane == 63) part[w] = x;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = part[i];
+    if (i < w) base += t;
+    total += t;
+  }
+  return base + x - v;
+}
+
 // Exclusive scan of hist[bh] (block-major, chunk-minor) in place, the block
 // starts, then the leaf-forward pieces: block beta with n pairs gets
 // ceil(n / kPieceFwd) pieces, numbered by an exclusive scan over beta, and
@@ -97,52 +124,50 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(BucketArgs a) {
   int* hh = a.hist + (int64_t)bh * n;
   const int64_t per = (n + 1023) / 1024;
   const int64_t s0 = tid * per, s1 = min(n, s0 + per);
+  // each thread's run of counts, kScanBatch loads in flight at a time
   int sum = 0;
-  for (int64_t i = s0; i < s1; ++i) sum += hh[i];
-  part[tid] = sum;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const int v = tid >= o ? part[tid - o] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  for (int64_t i0 = s0; i0 < s1; i0 += kScanBatch) {
+    int x[kScanBatch];
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) x[j] = i0 + j < s1 ? hh[i0 + j] : 0;
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) sum += x[j];
   }
-  int run = part[tid] - sum;
-  for (int64_t i = s0; i < s1; ++i) {
-    const int x = hh[i];
-    hh[i] = run;
-    run += x;
+  int total;
+  int run = block_scan_1024(sum, part, tid, total);
+  for (int64_t i0 = s0; i0 < s1; i0 += kScanBatch) {
+    int x[kScanBatch];
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) x[j] = i0 + j < s1 ? hh[i0 + j] : 0;
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j)
+      if (i0 + j < s1) {
+        hh[i0 + j] = run;
+        run += x[j];
+      }
   }
   __syncthreads();
   int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   for (int beta = tid; beta < a.NL; beta += 1024) bs[beta] = hh[(int64_t)beta * a.nchunk];
-  if (tid == 1023) bs[a.NL] = part[1023];
+  if (tid == 1023) bs[a.NL] = total;
   __syncthreads();  // block starts (global, this workgroup's writes) visible; part[] reused below
 
   const int perb = (a.NL + 1023) / 1024;
   const int b0 = min(a.NL, tid * perb), b1 = min(a.NL, b0 + perb);
   int np = 0;
   for (int beta = b0; beta < b1; ++beta) np += (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
-  part[tid] = np;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const int v = tid >= o ? part[tid - o] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
-  }
   int* ps = a.piece_start + (int64_t)bh * (a.NL + 1);
   int* pb = a.piece_block + (int64_t)bh * a.npiece;
-  int pr = part[tid] - np;
+  int npt;
+  int pr = block_scan_1024(np, part, tid, npt);
   for (int beta = b0; beta < b1; ++beta) {
     ps[beta] = pr;
     const int m = (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
     for (int j = 0; j < m; ++j) pb[pr + j] = beta;
     pr += m;
   }
-  const int total = part[1023];
-  if (tid == 1023) ps[a.NL] = total;
-  for (int i = total + tid; i < a.npiece; i += 1024) pb[i] = -1;
+  if (tid == 1023) ps[a.NL] = npt;
+  for (int i = npt + tid; i < a.npiece; i += 1024) pb[i] = -1;
 }
 
 hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
