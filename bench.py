@@ -33,7 +33,19 @@ CONFIGS = {
     "C2": (4, 4096, 16, 64, "bfloat16", 2, 64, 8, False, "normal"),
     "C3": (2, 16384, 16, 128, "bfloat16", 4, 64, 16, True, "normal"),
     "C4": (1, 131072, 8, 128, "bfloat16", 2, 128, 16, False, "scaled"),
+    "C5-D32": (8, 8192, 32, 32, "float16", 2, 32, 8, True, "skewed"),
+    "C5-D96": (8, 8192, 32, 96, "float16", 2, 32, 8, True, "skewed"),
 }
+
+
+def skew(q, k, gen, D):
+    """Student-t(3) keys and queries with a shared random direction x3 (the C5 stress inputs)."""
+    import torch
+
+    B, L, H, _ = k.shape
+    chi = sum(torch.randn((B, L, H, 1), device=k.device, generator=gen) ** 2 for _ in range(3)) / 3
+    u = torch.randn(D, device=k.device, generator=gen)
+    return (q.float() + 3 * u / u.norm()).to(q.dtype), (k.float() / chi.sqrt()).to(k.dtype)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK = {"bfloat16": 2500.0, "float16": 2500.0, "float32": 157.3}  # dense TFLOP/s
@@ -135,6 +147,8 @@ def det_main(args) -> int:
     q, k, v, do = (torch.randn((B, L, H, D), device=dev, dtype=dtype, generator=gen) for _ in range(4))
     if kind == "scaled":
         q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    elif kind == "skewed":
+        q, k = skew(q, k, gen, D)
     for x in (q, k, v):
         x.requires_grad_(True)
 
@@ -219,6 +233,8 @@ def main() -> int:
     q, k, v, do = (torch.randn(shape, device=dev, dtype=dtype, generator=gen) for _ in range(4))
     if kind == "scaled":
         q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    elif kind == "skewed":
+        q, k = skew(q, k, gen, D)
     q.requires_grad_(True)
     k.requires_grad_(True)
     v.requires_grad_(True)

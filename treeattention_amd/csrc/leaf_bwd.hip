@@ -239,22 +239,28 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   }
 }
 
-// Eight-wave variant for 16-bit inputs: 128-pair tiles.  Phase A (each wave,
+// Transposing-read variant for 16-bit inputs: eight waves and 128-pair tiles
+// (four waves and 64-pair tiles for 128-key blocks).  Phase A (each wave,
 // its 16 pairs): query and output-gradient rows come straight from global
 // memory into MFMA fragments (the next tile's are loaded while this one
 // computes), then P, delta, dz and the pair's dq; the wave then stores its
 // rows of Q, dout, wP and dz into row-major LDS tiles with 16- and 8-byte
-// writes.  Phase B (all waves, 2x2 output tiles each): dV += (wP)^T dout and
-// dK += dz^T Q over the tile's 128 pairs.  The MFMA operands of phase B and
+// writes.  Phase B (all waves, each a block of output tiles): dV += (wP)^T dout
+// and dK += dz^T Q over the tile's pairs.  The MFMA operands of phase B and
 // K^T of the dq product are read with ds_read_b64_tr_b16, gfx950's transposing
 // LDS read: within each group of 16 lanes, lane i receives element i%4 of the
 // 8-byte slots of lanes 4r + i/4 (r = 0..3), so pointing lane j of a group at
 // row k0 + j/4, columns 4(j%4).. of a row-major [k][n] tile gives lane i the
 // four values [k0..k0+3][n = i] -- a k-contiguous operand column.  Row strides
 // are padded by 16 elements so every 16-lane group touches distinct banks.
+// Leaf blocks of 128 keys run with four waves and 64-pair tiles (the K / V,
+// pair-row and P / dz tiles then fit the LDS, and each wave's quarter of
+// dV / dK becomes a key half with all head dims, accumulated at one wave per
+// SIMD); smaller blocks with eight waves and 128-pair tiles.
 template <int D, int LBP>
 struct BwdTrTile {
-  static constexpr int QT = 128;
+  static constexpr int NW = LBP > 64 ? 4 : 8;  // waves
+  static constexpr int QT = 16 * NW;           // pairs per tile, 16 per wave
   static constexpr int RS = D + 16, PS = LBP + 16;
   static constexpr int bytes = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
 };
@@ -278,12 +284,12 @@ struct PairRows {
 };
 
 template <typename E, int D, int LBP>
-__global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
+__global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
   static_assert(sizeof(E) == 2, "16-bit inputs");
   using M = Mfma<E>;
   using BT = BwdTrTile<D, LBP>;
   constexpr int QT = BT::QT, RS = BT::RS, PS = BT::PS;
-  constexpr int NW = 8;
+  constexpr int NW = BT::NW;
   extern __shared__ __align__(16) char smem[];
   E* Ks = (E*)smem;        // [LBP][RS]
   E* Vs = Ks + LBP * RS;   // [LBP][RS]
@@ -329,12 +335,15 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
   }
   __syncthreads();
 
-  // phase B: waves 0-3 accumulate dV = (wP)^T dout, waves 4-7 dK = dz^T Q;
-  // wave w & 3 owns the quarter (key half (w & 3) >> 1, dim half w & 1):
-  // MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand reads per MK2 * ND2 MFMAs
-  constexpr int MK2 = LBP / 32, ND2 = D / 32;
-  const bool dkw = w >= 4;
-  const int mkb = MK2 * ((w & 3) >> 1), ndb = ND2 * (w & 1);
+  // phase B: the first half of the waves accumulates dV = (wP)^T dout, the
+  // second dK = dz^T Q; with eight waves wave w & 3 owns the quarter (key half
+  // (w & 3) >> 1, dim half w & 1), with four waves wave w & 1 owns key half
+  // w & 1 and every head dim: MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand
+  // reads per MK2 * ND2 MFMAs
+  constexpr int MK2 = LBP / 32, ND2 = NW == 8 ? D / 32 : D / 16;
+  const int wm = w % (NW / 2);
+  const bool dkw = w >= NW / 2;
+  const int mkb = NW == 8 ? MK2 * (wm >> 1) : MK2 * wm, ndb = NW == 8 ? ND2 * (wm & 1) : 0;
   const E* Ab = dkw ? Zs : Ps;
   const E* Bb = dkw ? Qs : Gs;
   f32x4 acc[MK2][ND2];
@@ -343,7 +352,7 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
 #pragma unroll
     for (int y = 0; y < ND2; ++y) acc[x][y] = zero4();
 
-  // Software pipeline over 128-pair tiles with two register sets: a tile
+  // Software pipeline over QT-pair tiles with two register sets: a tile
   // first waits for its own set (loaded one tile earlier), then issues the
   // loads of the next tile into the other set and reads the pair index of the
   // tile after.  The wait sits before the new loads on purpose: vmcnt counts
@@ -476,7 +485,7 @@ __global__ __launch_bounds__(512) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
     }
     __syncthreads();
 
-    // ---- phase B: this wave's quarter of dV or dK over the tile's 128 pairs
+    // ---- phase B: this wave's block of dV or dK over the tile's pairs
 #pragma unroll
     for (int ks = 0; ks < QT / M::K; ++ks) {
       const int ka = 32 * ks + 8 * g, kb = ka + 4;
@@ -569,11 +578,11 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
   const unsigned grid = xcd_grid(P.BH, P.geo.NL);
   constexpr int smem8 = BwdTrTile<D, LBP>::bytes;
-  if constexpr (sizeof(E) == 2 && LBP <= 64 && LBP >= 32 && smem8 <= 160 * 1024) {
+  if constexpr (sizeof(E) == 2 && LBP >= 32 && smem8 <= 160 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_tr_kernel<E, D, LBP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem8);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((leaf_bwd_tr_kernel<E, D, LBP>), dim3(grid), dim3(512), smem8, st, a);
+    hipLaunchKernelGGL((leaf_bwd_tr_kernel<E, D, LBP>), dim3(grid), dim3(64 * BwdTrTile<D, LBP>::NW), smem8, st, a);
   } else {
     const int smem = bwd_smem_t<E, D, LBP>();
     hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,
