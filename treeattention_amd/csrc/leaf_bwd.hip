@@ -253,14 +253,14 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
 // row k0 + j/4, columns 4(j%4).. of a row-major [k][n] tile gives lane i the
 // four values [k0..k0+3][n = i] -- a k-contiguous operand column.  Row strides
 // are padded by 16 elements so every 16-lane group touches distinct banks.
-// Leaf blocks of 128 keys run with four waves and 64-pair tiles (the K / V,
-// pair-row and P / dz tiles then fit the LDS, and each wave's quarter of
-// dV / dK becomes a key half with all head dims, accumulated at one wave per
-// SIMD); smaller blocks with eight waves and 128-pair tiles.
+// Eight waves.  Leaf blocks of up to 64 keys take 128-pair tiles, 16 pairs
+// per wave; 128-key blocks take 64-pair tiles (so the K / V, pair-row and
+// P / dz tiles fit the LDS), whose phase A runs on waves 0-3 while all eight
+// share phase B.
 template <int D, int LBP>
 struct BwdTrTile {
-  static constexpr int NW = LBP > 64 ? 4 : 8;  // waves
-  static constexpr int QT = 16 * NW;           // pairs per tile, 16 per wave
+  static constexpr int NW = 8;                      // waves
+  static constexpr int QT = LBP > 64 ? 64 : 128;    // pairs per tile, 16 per phase-A wave
   static constexpr int RS = D + 16, PS = LBP + 16;
   static constexpr int bytes = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
 };
@@ -335,15 +335,12 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kern
   }
   __syncthreads();
 
-  // phase B: the first half of the waves accumulates dV = (wP)^T dout, the
-  // second dK = dz^T Q; with eight waves wave w & 3 owns the quarter (key half
-  // (w & 3) >> 1, dim half w & 1), with four waves wave w & 1 owns key half
-  // w & 1 and every head dim: MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand
-  // reads per MK2 * ND2 MFMAs
-  constexpr int MK2 = LBP / 32, ND2 = NW == 8 ? D / 32 : D / 16;
-  const int wm = w % (NW / 2);
-  const bool dkw = w >= NW / 2;
-  const int mkb = NW == 8 ? MK2 * (wm >> 1) : MK2 * wm, ndb = NW == 8 ? ND2 * (wm & 1) : 0;
+  // phase B: waves 0-3 accumulate dV = (wP)^T dout, waves 4-7 dK = dz^T Q;
+  // wave w & 3 owns the quarter (key half (w & 3) >> 1, dim half w & 1):
+  // MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand reads per MK2 * ND2 MFMAs
+  constexpr int MK2 = LBP / 32, ND2 = D / 32;
+  const bool dkw = w >= 4;
+  const int mkb = MK2 * ((w & 3) >> 1), ndb = ND2 * (w & 1);
   const E* Ab = dkw ? Zs : Ps;
   const E* Bb = dkw ? Qs : Gs;
   f32x4 acc[MK2][ND2];
@@ -360,7 +357,8 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kern
   // them.  The loop is unrolled twice so the sets never move between registers.
   const int* ord = a.order + (int64_t)bh * LS;
   const int pcol = 16 * w + col;  // this lane's pair column within the tile
-  auto idx = [&](int t) { return t + pcol < end ? ord[t + pcol] : -1; };
+  const bool aw = QT == 16 * NW || 16 * w < QT;  // the wave has pairs (phase A)
+  auto idx = [&](int t) { return aw && t + pcol < end ? ord[t + pcol] : -1; };
   auto fetch = [&](int e, PairRows<E, D>& r) {  // pair entry e = l * S + u, or -1
     const int l = e >= 0 ? e / S : 0;
     r.l = e >= 0 ? l : -1;
@@ -379,6 +377,7 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kern
 
     // ---- phase A: this wave's 16 pairs
     f32x4 sacc[LBP / 16], pacc[LBP / 16];
+    if (aw) {
 #pragma unroll
     for (int mt = 0; mt < LBP / 16; ++mt) {
       sacc[mt] = zero4();
@@ -461,8 +460,10 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kern
       }
     }
 
+    }  // aw
+
     __syncthreads();  // phase B of the previous tile is done with the staging tiles
-    {
+    if (aw) {
       E* pr = Ps + pcol * PS + 4 * g;
       E* zr = Zs + pcol * PS + 4 * g;
 #pragma unroll
