@@ -347,7 +347,7 @@ __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols
 //   dq^T += C_chunk^T G^T (wave w: head-dim tiles w, w+4, ...)
 // and G^T goes to global for the summary-gradient product.  The epilogue adds
 // the leaf parts dq_pair of each query's distinct blocks.
-// kP: lanes per query in build_g (16: S <= 16, DPP scans; 64: shuffles).
+// kP: lanes per query in build_g (8: S <= 8, 16: S <= 16, DPP scans; 64: shuffles).
 // kB: the branching factor when known at compile time (2 or 4), else 0.
 template <typename E, int D, int kP, int kB>
 __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
@@ -838,6 +838,8 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   };
   hipError_t e = hipSuccess;
   if (P.S > 16) e = launch_dq(tree_dq_kernel<E, D, 64, 0>);
+  else if (P.S <= 8 && P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 8, 2>);  // half the scan lanes
+  else if (P.S <= 8 && P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 8, 4>);
   else if (P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 16, 4>);
   else if (P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 16, 2>);
   else e = launch_dq(tree_dq_kernel<E, D, 16, 0>);
