@@ -175,6 +175,8 @@ struct TileSmem {
   int* lf;     // [64][S]
   float* dls;  // [64][S]
   int* cn;     // [64]
+  float* scv;  // [64 * 16][2] per scan lane of a level: A_row, A_n (S <= 16)
+  int* sci;    // [64 * 16][3] per scan lane: child row, node, run-end flags | children mask << 8
 };
 
 template <typename E>
@@ -213,6 +215,112 @@ template <int P>
 __device__ __forceinline__ int grp_down1(int x) {
   if constexpr (P <= 16) return row_shl1(x);
   else return __shfl_down(x, 1, P);
+}
+
+// build_g_p in two halves for levels wider than one chunk (P <= 16, b = 2 or
+// 4): build_g_scan runs the segmented scans of depth d once and keeps each
+// lane's sums and run flags in LDS; build_g_emit then writes each chunk's
+// entries from them.  Every lane reads back only what it wrote itself.
+template <typename E, int P, int kB>
+__device__ __forceinline__ void build_g_scan(const Geo& G, int d, int S, int nq, const int* lf, const float* dls,
+                                             const int* cn, float* scv, int* sci, int tid) {
+  static_assert(P <= 16 && (kB == 2 || kB == 4), "hoisted scans: P <= 16, b = 2 or 4");
+  constexpr int LP = P <= 1 ? 0 : P <= 2 ? 1 : P <= 4 ? 2 : P <= 8 ? 3 : 4;
+  constexpr int lb = kB == 2 ? 1 : 2;
+  const int sh = lb * (G.T - d), sh2 = sh - lb;
+  const int lane = tid & 63;
+  for (int e0 = 0; e0 < (kQueryTile << LP); e0 += 256) {
+    const int e = e0 + tid;
+    const int qi = e >> LP, u = e & (P - 1);
+    const int cnt = qi < nq ? cn[qi] : 0;
+    const bool act = u < cnt;
+    const int leaf = act ? lf[qi * S + u] : 0;
+    const float dl = act ? dls[qi * S + u] : 0.f;
+    const int crow = act ? (leaf >> sh2) : -1 - u;
+    const int node = act ? (leaf >> sh) : -1 - u;
+    float vc = dl, vn = dl;
+    int has0 = act ? 1 << (crow & (kB - 1)) : 0;
+    auto step = [&](auto oc) {
+      constexpr int O = decltype(oc)::value;
+      if constexpr (O < P) {
+        const float tc = grp_up<P, O>(vc);
+        const float tn = grp_up<P, O>(vn);
+        const int kc = grp_up<P, O>(crow);
+        const int kn = grp_up<P, O>(node);
+        const int h0 = grp_up<P, O>(has0);
+        if (u >= O) {
+          if (kc == crow) vc += tc;
+          if (kn == node) {
+            vn += tn;
+            has0 |= h0;
+          }
+        }
+      }
+    };
+    step(std::integral_constant<int, 1>());
+    step(std::integral_constant<int, 2>());
+    step(std::integral_constant<int, 4>());
+    step(std::integral_constant<int, 8>());
+    const int nxc = grp_down1<P>(crow);
+    const int nxn = grp_down1<P>(node);
+    const bool last = u + 1 >= cnt;
+    const bool cend = act && (last || nxc != crow);
+    const bool nend = act && (last || nxn != node);
+    const uint64_t rest = __ballot(nend) >> lane;
+    const int src = rest ? lane + __builtin_ctzll(rest) : lane;
+    const float An = __shfl(vn, src, 64);
+    scv[2 * e] = vc;
+    scv[2 * e + 1] = An;
+    sci[3 * e] = crow;
+    sci[3 * e + 1] = node;
+    sci[3 * e + 2] = (cend ? 1 : 0) | (nend ? 2 : 0) | (has0 << 8);
+  }
+}
+
+template <typename E, int P, int kB>
+__device__ __forceinline__ void build_g_emit(const Geo& G, int c0, int ncols, float maxhalf, const float* Xs,
+                                             const float* scv, const int* sci, E* Gm, int tid) {
+  constexpr int LP = P <= 1 ? 0 : P <= 2 ? 1 : P <= 4 ? 2 : P <= 8 ? 3 : 4;
+  constexpr int lb = kB == 2 ? 1 : 2;
+  for (int e0 = 0; e0 < (kQueryTile << LP); e0 += 256) {
+    const int e = e0 + tid;
+    const int qi = e >> LP;
+    const int fl = sci[3 * e + 2];
+    const bool cend = fl & 1, nend = fl & 2;
+    const int node = sci[3 * e + 1];
+    const int base = (node << lb) - c0;
+    if ((cend || nend) && base >= 0 && base < ncols) {
+      const int crow = sci[3 * e], has0 = fl >> 8;
+      const float vc = scv[2 * e], An = scv[2 * e + 1];
+      const float* xr = Xs + qi * kXS + base;
+      E* gr = Gm + qi * kGS + base;
+      float xv[kB], ev[kB];
+      if constexpr (kB == 4) {
+        const float4 t = *(const float4*)xr;
+        xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
+      } else {
+        const float2 t = *(const float2*)xr;
+        xv[0] = t.x; xv[1] = t.y;
+      }
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < kB; ++j) mx = fmaxf(mx, clamp_h(xv[j], maxhalf));
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        ev[j] = __expf(clamp_h(xv[j], maxhalf) - mx);
+        se += ev[j];
+      }
+      const float pa = An / se;
+      const int jc = crow & (kB - 1);
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const bool live = xv[j] >= -maxhalf && xv[j] <= maxhalf;
+        if (cend && j == jc) gr[j] = (E)(live ? vc - ev[j] * pa : 0.f);
+        else if (nend && !((has0 >> j) & 1)) gr[j] = (E)(live ? -ev[j] * pa : 0.f);
+      }
+    }
+  }
 }
 
 // G for depth d, chunk [c0, c0 + ncols) of the level's child rows, into
@@ -370,6 +478,8 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   sm.lf = (int*)(sm.Gm + kQueryTile * kGS);
   sm.dls = (float*)(sm.lf + kQueryTile * S);
   sm.cn = (int*)(sm.dls + kQueryTile * S);
+  sm.scv = (float*)(sm.cn + kQueryTile);
+  sm.sci = (int*)(sm.scv + 2 * kQueryTile * 16);
 
   RowFrags<E, D> qa[4];
 #pragma unroll
@@ -501,7 +611,16 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       z8(sm.Gm + r * kGS + cc);
     }
     __syncthreads();
-    if (rcols > 0) build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    if constexpr (kP <= 16 && (kB == 2 || kB == 4)) {
+      if (lvl > kChunk) {  // the level's scans once, at its first chunk
+        if (c0 == 0) build_g_scan<E, kP, kB>(G, d, S, nq, sm.lf, sm.dls, sm.cn, sm.scv, sm.sci, tid);
+        if (rcols > 0) build_g_emit<E, kP, kB>(G, c0, rcols, a.maxhalf, sm.Xs, sm.scv, sm.sci, sm.Gm, tid);
+      } else if (rcols > 0) {
+        build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+      }
+    } else if (rcols > 0) {
+      build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+    }
     __syncthreads();
     if (a.refc) {
       // boundary-mass gradient of the reference causal mode (ref_causal_grad_kernel)
@@ -776,7 +895,9 @@ __global__ __launch_bounds__(256) void nodekeys_adjoint_kernel(TreeArgs a) {
 
 static int tree_smem(const Plan& P) {
   const int S = (int)P.S;
-  return kQueryTile * kXS * 4 + kQueryTile * kGS * P.esize + kQueryTile * S * 8 + kQueryTile * 4;
+  // + the hoisted scan lanes (S <= 16): two floats and three ints each
+  return kQueryTile * kXS * 4 + kQueryTile * kGS * P.esize + kQueryTile * S * 8 + kQueryTile * 4 +
+         (S <= 16 ? kQueryTile * 16 * 20 : 0);
 }
 
 template <typename E, int D>
