@@ -189,6 +189,12 @@ def test_odd_leaf_blocks_and_partial_query_tiles(b, LB, L, D, causal, dtype):
     run_case(2, L, 2, D, 8, b, LB, "natural", causal, dtype)
 
 
+def test_large_bucket_histogram():
+    # 4096 leaf blocks x 64 query chunks: the bucket counts are scanned in
+    # segments by several workgroups per (batch, head)
+    run_case(1, 16384, 1, 32, 4, 4, 4, "natural", False, torch.bfloat16)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_fewer_queries_than_keys(causal):
     # L = 256 queries over N = 1024 keys (causal: bottom-right aligned)

@@ -17,7 +17,7 @@ constexpr int kWin = 2048;                 // leaf blocks per LDS window
 constexpr int kWords = kQueryChunk / 32;  // bitmask words per block
 
 struct BucketArgs {
-  int L, H, S, NL, nchunk, npiece;
+  int L, H, S, NL, nchunk, npiece, nseg;
   const int* slot_leaf;
   const int* slot_count;
   int* hist;         // (BH, NL, nchunk)
@@ -25,6 +25,7 @@ struct BucketArgs {
   int* order;        // (BH, L*S)
   int* piece_start;  // (BH, NL+1)
   int* piece_block;  // (BH, npiece)
+  int* seg_sum;      // (BH, nseg) large histograms: counts per scan segment
 };
 
 // grid (nchunk, BH), block kQueryChunk (one thread per query of the chunk).
@@ -112,6 +113,29 @@ __device__ __forceinline__ int block_scan_1024(int v, int* part, int tid, int& t
   return base + x - v;
 }
 
+// The leaf-forward pieces from the block starts bs: block beta with n pairs
+// gets ceil(n / kPieceFwd) pieces, numbered by an exclusive scan over beta,
+// and piece_block names each piece's block (-1 past the last).  All 1024
+// threads call it.
+__device__ __forceinline__ void bucket_pieces(const BucketArgs& a, int bh, const int* bs, int* part, int tid) {
+  const int perb = (a.NL + 1023) / 1024;
+  const int b0 = min(a.NL, tid * perb), b1 = min(a.NL, b0 + perb);
+  int np = 0;
+  for (int beta = b0; beta < b1; ++beta) np += (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
+  int* ps = a.piece_start + (int64_t)bh * (a.NL + 1);
+  int* pb = a.piece_block + (int64_t)bh * a.npiece;
+  int npt;
+  int pr = block_scan_1024(np, part, tid, npt);
+  for (int beta = b0; beta < b1; ++beta) {
+    ps[beta] = pr;
+    const int m = (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
+    for (int j = 0; j < m; ++j) pb[pr + j] = beta;
+    pr += m;
+  }
+  if (tid == 1023) ps[a.NL] = npt;
+  for (int i = npt + tid; i < a.npiece; i += 1024) pb[i] = -1;
+}
+
 // Exclusive scan of hist[bh] (block-major, chunk-minor) in place, the block
 // starts, then the leaf-forward pieces: block beta with n pairs gets
 // ceil(n / kPieceFwd) pieces, numbered by an exclusive scan over beta, and
@@ -152,22 +176,69 @@ __global__ __launch_bounds__(1024) void bucket_scan_kernel(BucketArgs a) {
   if (tid == 1023) bs[a.NL] = total;
   __syncthreads();  // block starts (global, this workgroup's writes) visible; part[] reused below
 
-  const int perb = (a.NL + 1023) / 1024;
-  const int b0 = min(a.NL, tid * perb), b1 = min(a.NL, b0 + perb);
-  int np = 0;
-  for (int beta = b0; beta < b1; ++beta) np += (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
-  int* ps = a.piece_start + (int64_t)bh * (a.NL + 1);
-  int* pb = a.piece_block + (int64_t)bh * a.npiece;
-  int npt;
-  int pr = block_scan_1024(np, part, tid, npt);
-  for (int beta = b0; beta < b1; ++beta) {
-    ps[beta] = pr;
-    const int m = (bs[beta + 1] - bs[beta] + kPieceFwd - 1) / kPieceFwd;
-    for (int j = 0; j < m; ++j) pb[pr + j] = beta;
-    pr += m;
-  }
-  if (tid == 1023) ps[a.NL] = npt;
-  for (int i = npt + tid; i < a.npiece; i += 1024) pb[i] = -1;
+  bucket_pieces(a, bh, bs, part, tid);
+}
+
+// Large histograms (many leaf blocks x query chunks): the scan runs over
+// segments of kSegScan counts, 16 per thread of a 1024-thread workgroup:
+// bucket_segsum_kernel sums each segment, bucket_segscan_kernel adds the sums
+// of the segments before its own and rescans it in place (writing the block
+// starts that fall in it), bucket_pieces_kernel builds the piece table.
+constexpr int kSegScan = 1024 * kScanBatch;
+
+__global__ __launch_bounds__(1024) void bucket_segsum_kernel(BucketArgs a) {
+  __shared__ int part[16];
+  const int seg = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const int64_t n = (int64_t)a.NL * a.nchunk;
+  const int* hh = a.hist + (int64_t)bh * n;
+  const int64_t s0 = (int64_t)seg * kSegScan + tid * kScanBatch;
+  int x[kScanBatch], sum = 0;
+#pragma unroll
+  for (int j = 0; j < kScanBatch; ++j) x[j] = s0 + j < n ? hh[s0 + j] : 0;
+#pragma unroll
+  for (int j = 0; j < kScanBatch; ++j) sum += x[j];
+  int total;
+  block_scan_1024(sum, part, tid, total);
+  if (tid == 0) a.seg_sum[(int64_t)bh * a.nseg + seg] = total;
+}
+
+__global__ __launch_bounds__(1024) void bucket_segscan_kernel(BucketArgs a) {
+  __shared__ int part[16];
+  __shared__ int offs;
+  const int seg = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const int64_t n = (int64_t)a.NL * a.nchunk;
+  int* hh = a.hist + (int64_t)bh * n;
+  const int* ss = a.seg_sum + (int64_t)bh * a.nseg;
+  // the sums of the earlier segments
+  int pre = 0;
+  for (int i = tid; i < seg; i += 1024) pre += ss[i];
+  int ptot;
+  block_scan_1024(pre, part, tid, ptot);
+  if (tid == 0) offs = ptot;
+  const int64_t s0 = (int64_t)seg * kSegScan + tid * kScanBatch;
+  int x[kScanBatch], sum = 0;
+#pragma unroll
+  for (int j = 0; j < kScanBatch; ++j) x[j] = s0 + j < n ? hh[s0 + j] : 0;
+#pragma unroll
+  for (int j = 0; j < kScanBatch; ++j) sum += x[j];
+  int total;
+  int run = block_scan_1024(sum, part, tid, total);  // its barriers also publish offs
+  run += offs;
+  int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
+#pragma unroll
+  for (int j = 0; j < kScanBatch; ++j)
+    if (s0 + j < n) {
+      hh[s0 + j] = run;
+      if ((s0 + j) % a.nchunk == 0) bs[(s0 + j) / a.nchunk] = run;
+      run += x[j];
+    }
+  if (seg == a.nseg - 1 && tid == 1023) bs[a.NL] = offs + total;
+}
+
+__global__ __launch_bounds__(1024) void bucket_pieces_kernel(BucketArgs a) {
+  __shared__ int part[16];
+  const int bh = blockIdx.x;
+  bucket_pieces(a, bh, a.block_start + (int64_t)bh * (a.NL + 1), part, threadIdx.x);
 }
 
 hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
@@ -185,8 +256,16 @@ hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
   a.npiece = P.npiece;
   a.piece_start = (int*)(rec + P.rec.piece_start);
   a.piece_block = (int*)(rec + P.rec.piece_block);
+  a.nseg = P.nseg;
+  a.seg_sum = (int*)(rec + P.rec.seg_sum);
   hipLaunchKernelGGL(bucket_pass_kernel<false>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
-  hipLaunchKernelGGL(bucket_scan_kernel, dim3(P.BH), dim3(1024), 0, st, a);
+  if (P.nseg > 4) {
+    hipLaunchKernelGGL(bucket_segsum_kernel, dim3(P.nseg, P.BH), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(bucket_segscan_kernel, dim3(P.nseg, P.BH), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(bucket_pieces_kernel, dim3(P.BH), dim3(1024), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(bucket_scan_kernel, dim3(P.BH), dim3(1024), 0, st, a);
+  }
   hipLaunchKernelGGL(bucket_pass_kernel<true>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
   return hipGetLastError();
 }

@@ -144,6 +144,8 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.order = r.take(P->BH * L * S * 4);
   P->rec.piece_start = r.take(P->BH * (NL + 1) * 4);
   P->rec.piece_block = r.take(P->BH * P->npiece * 4);
+  P->nseg = (int)((NL * P->nchunk + 16383) / 16384);  // segments of 1024 threads x 16 counts
+  P->rec.seg_sum = r.take(P->BH * P->nseg * 4);
   P->rec.dstar = r.take(p->causal == TA_CAUSAL_REFERENCE ? L * 4 : 0);
   P->rec.total = r.at;
   Carver f;

@@ -505,6 +505,7 @@ struct RecordLayout {
   int64_t order;       // int (BH, L*S): (l*S + u) grouped by leaf block
   int64_t piece_start; // int (BH, NL + 1): first leaf-forward piece of each block, exclusive scan
   int64_t piece_block; // int (BH, npiece): leaf block of each piece, -1 past the last
+  int64_t seg_sum;     // int (BH, nseg): bucket counts per histogram scan segment
   int64_t dstar;       // int (L): reference causal mode: first uncorrected depth per query
   int64_t total;
 };

@@ -14,6 +14,7 @@ struct Plan {
   int qc;           // queries per bucketing chunk
   int nchunk;       // bucketing chunks per (batch, head)
   int npiece;       // leaf-forward pieces per (batch, head), upper bound
+  int nseg;         // scan segments of the bucket histogram per (batch, head)
   int64_t Lp;       // L rounded up to a multiple of kQueryTile
   int qsplit;       // query splits of the summary-gradient product
   RecordLayout rec;
