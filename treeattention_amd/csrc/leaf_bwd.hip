@@ -542,7 +542,12 @@ static int bwd_smem_t() {
 
 int leaf_bwd_smem(const Plan& P) {
   const int D = (int)P.D, LBP = padded_keys(P.geo.LB), ES = P.esize;
-  const bool kt = (LBP <= 64) || (ES == 2 && D <= 64);
+  if (ES == 2) {  // the transposing-read kernel (BwdTrTile)
+    const int QT = LBP > 64 ? 64 : 128, RS = D + 16, PS = LBP + 16;
+    const int s = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
+    return s <= 160 * 1024 ? s : -1;
+  }
+  const bool kt = LBP <= 64;
   const int s = (2 * LBP * (D + 8) + 2 * 64 * (D + 8) + 2 * LBP * 72 + (kt ? D * (LBP + 8) : 0)) * ES + 64 * 4;
   return s <= 160 * 1024 ? s : -1;
 }
