@@ -123,3 +123,58 @@ def test_full_size(name):
         r = rel(f64(dq)[:, -SUB:], dq_o)
         print(f"  (b={bb}, h={h}) clean {clean.mean():.3f}, dq rel err {r:.3g}", flush=True)
         assert r < 2e-2
+
+
+# Deterministic (exact) mode through the attn-bench adapter at the C2 and C3
+# shapes: the streaming kernels, no (L, N) buffer.
+DET_FULL = {
+    "C2-shape": (4, 4096, 16, 64, False),
+    "C3-shape": (2, 16384, 16, 128, True),
+}
+
+
+@pytest.mark.parametrize("name", sorted(DET_FULL))
+def test_deterministic_adapter_full_size(name, monkeypatch):
+    """Full-size adapter path with TREEATTN_NUM_SAMPLES unset: the identities
+    sum_n dv_n = sum_l dout_l (each query's exact weights sum to one) and
+    sum_n dk_n = 0 (the Haar node keys drop every shift of the keys) per
+    (batch, head), and out / dq rows of the last 64 queries of two heads
+    against the float64 restatement (``ref_torch.leaf_logprobs``, softmax over
+    the visible leaves when causal, autograd for dq)."""
+    import treeattention_amd as ta
+    from oracle import ref_torch as R
+
+    monkeypatch.delenv("TREEATTN_NUM_SAMPLES", raising=False)
+    for var in ("TREEATTN_BRANCHING", "TREEATTN_LEAF_BLOCK", "TREEATTN_TREE_MODE"):
+        monkeypatch.delenv(var, raising=False)
+    B, L, H, D, causal = DET_FULL[name]
+    print(f"[case] deterministic adapter full size {name}: B={B} L={L} H={H} D={D} causal={causal}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q, k, v, do = (torch.randn(B, L, H, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(4))
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = ta.attn_fn(qg, kg, vg, causal, None)
+    out.backward(do)
+    torch.cuda.synchronize()
+    for t in (out, qg.grad, kg.grad, vg.grad):
+        assert torch.isfinite(t.float()).all()
+    assert rel(vg.grad.float().sum(1).cpu().numpy(), do.float().sum(1).cpu().numpy()) < 2e-2
+    dkf = kg.grad.float()
+    assert (dkf.sum(1).norm(dim=-1) / dkf.pow(2).sum((1, 3)).sqrt()).max().item() < 2e-2
+
+    for bb, h in ((0, 0), (B - 1, H - 1)):
+        to64 = lambda t: t[bb:bb + 1, :, h:h + 1].double().cpu().permute(1, 0, 2, 3)  # (L, 1, 1, D)
+        kq, vq = to64(k), to64(v)
+        kn = torch.from_numpy(O.haar_inorder(kq.numpy()))  # (L-1, 1, 1, D) heap-ordered node keys
+        qs = to64(q)[-SUB:].clone().requires_grad_(True)
+        lpp = R.leaf_logprobs(qs, kn)  # (SUB, 1, 1, L)
+        if causal:
+            vis = torch.arange(L).view(1, L) <= torch.arange(L - SUB, L).view(SUB, 1)
+            w = torch.softmax(lpp.masked_fill(~vis[:, None, None, :], float("-inf")), dim=-1)
+        else:
+            w = torch.exp(lpp)
+        o_ref = torch.einsum("lbhn,nbhd->lbhd", w, vq)
+        o_ref.backward(to64(do)[-SUB:])
+        assert rel(to64(out.detach())[-SUB:].numpy(), o_ref.detach().numpy()) < 2e-2
+        r = rel(to64(qg.grad)[-SUB:].numpy(), qs.grad.numpy())
+        print(f"  (b={bb}, h={h}) dq rel err {r:.3g}", flush=True)
+        assert r < 2e-2
