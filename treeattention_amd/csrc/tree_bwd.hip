@@ -15,7 +15,8 @@
 //   tree_dq_kernel: dq = sum_u dq_pair[u] + sum_chunks G C_chunk (MFMA); it
 //     also writes G^T and Q^T with the queries contiguous;
 //   tree_dc_kernel: dC = G^T Q per query split, a plain MFMA product of the
-//     two (no recomputation of logits or G);
+//     two (no recomputation of logits or G), skipping under exact causal
+//     masking the (row tile, query block) pairs whose G^T rows are all zero;
 //   dsum_reduce_kernel adds the splits in order;
 //   pool_adjoint_kernel: dk = dk_leaf + (summaries map)^T dC, which for
 //   compat summaries is the transpose of the reference's Haar keys
@@ -532,8 +533,9 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   F at[NMD][KT];
   // Exact causal restriction: every sampled block is <= blk_hi, so only
   // children of depth-d nodes over those blocks hold G entries for this tile;
-  // the products skip the other columns, whose G^T rows are still written as
-  // zeros.  (The reference causal mode samples past the query's position.)
+  // the products skip the other columns, and their G^T rows past the reach
+  // (rounded up to 32) are not written: tree_dc_kernel skips them by the same
+  // rule.  (The reference causal mode samples past the query's position.)
   const bool cz = a.causal;
   const int blk_hi = (l0 + nq - 1 + (a.N - a.L)) / G.LB;
   auto reach = [&](int d) {
@@ -575,9 +577,8 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   while (d < T) {
     const int lam = d + 1, lvl = G.pw[lam];
     const int ncols = min(kChunk, lvl - c0);
-    const int kcols = (ncols + 31) / 32 * 32;  // inside the level's zero padding
     const int rcols = max(0, min(ncols, reach(d) - c0));  // columns that can be nonzero
-    const int rk = (rcols + 31) / 32 * 32;
+    const int rk = (rcols + 31) / 32 * 32;  // inside the level's zero padding
     int nd = d, nc0 = c0 + kChunk;
     if (nc0 >= lvl) {
       nc0 = 0;
@@ -606,8 +607,8 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
 #pragma unroll
       for (int ks = 0; ks < KT; ++ks) asm volatile("" ::"v"(at[i][ks]) : "memory");
     if (nd < T) load_af(nd, nc0);
-    for (int e = tid; e < kQueryTile * kcols / 8; e += 256) {
-      const int r = e / (kcols / 8), cc = (e - r * (kcols / 8)) * 8;
+    for (int e = tid; e < kQueryTile * rk / 8; e += 256) {
+      const int r = e / (rk / 8), cc = (e - r * (rk / 8)) * 8;
       z8(sm.Gm + r * kGS + cc);
     }
     __syncthreads();
@@ -642,10 +643,11 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       __syncthreads();
     }
     {
-      // G^T rows of the chunk (kcols covers the level's zero padding rows),
-      // eight queries per 16-byte store
+      // G^T rows of the chunk up to the reach (without the causal restriction
+      // rk covers the chunk rounded up to 32 rows, the level's zero padding
+      // included), eight queries per 16-byte store
       E* gt = (E*)a.gt + ((int64_t)bh * rows + G.off[lam] + c0) * a.Lp + l0;
-      for (int e = tid; e < kcols * (kQueryTile / 8); e += 256) {
+      for (int e = tid; e < rk * (kQueryTile / 8); e += 256) {
         const int cc = e >> 3, q0 = (e & 7) * 8;
         E v8[8];
 #pragma unroll
@@ -720,6 +722,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
 // G^T row is read once, straight from global memory into MFMA fragments.
 constexpr int kDcRows = 3;   // row tiles per wave
 constexpr int kDcKB = 64;    // queries per staged block (whole 128-byte lines of G^T rows)
+static_assert(kDcKB == kQueryTile, "a staged query block is one tree_dq_kernel tile (the causal row rule)");
 
 template <typename E, int D>
 __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
@@ -739,6 +742,47 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   const int64_t k0 = (int64_t)split * per, k1 = min(Lp, k0 + per);
   const int rt0 = chunk * 8 * kDcRows + w;
   const E* gt = (const E*)a.gt + (int64_t)bh * rows * Lp;
+  // Exact causal mode: tree_dq_kernel writes the G^T row of column c of level
+  // lam for a query block only where (c & ~31) is below that block's reach,
+  // i.e. where ((c & ~31) >> lb) << lb (T - lam + 1) <= blk_hi, the block's
+  // last reachable leaf block; other rows may hold stale data and are neither
+  // read nor multiplied.  thr() is that bound per row; the loop starts at the
+  // first query block any tile of this chunk needs (blk_hi grows with kb).
+  const Geo& G = a.geo;
+  const bool cz = a.causal;
+  auto thr = [&](int lam, int r) { return (((r - G.off[lam]) & ~31) >> G.lb) << (G.lb * (G.T - lam + 1)); };
+  auto level_of = [&](int r) {
+    int lam = 1;
+    while (lam < G.T && r >= G.off[lam + 1]) ++lam;
+    return lam;
+  };
+  auto bhi = [&](int64_t kb) {
+    const int l0 = (int)kb, nq = min(kQueryTile, a.L - l0);
+    return (l0 + nq - 1 + (a.N - a.L)) / G.LB;
+  };
+  int th[kDcRows];
+#pragma unroll
+  for (int i = 0; i < kDcRows; ++i) {
+    const int r = 16 * (rt0 + 8 * i);
+    th[i] = cz && r < rows ? thr(level_of(r), r) : 0;
+  }
+  int64_t ks0 = k0;
+  if (cz && k0 < k1) {
+    const int r0 = chunk * 8 * kDcRows * 16, r1 = min(rows, r0 + 8 * kDcRows * 16);
+    int mth = 0x7fffffff;
+    for (int lam = 1; lam <= G.T; ++lam) {
+      const int lo = max(r0, G.off[lam]), hi = min(r1, G.off[lam + 1]);
+      if (lo < hi) mth = min(mth, thr(lam, lo));
+    }
+    int64_t lo = k0 / kDcKB, hi = k1 / kDcKB;  // first block in [lo, hi) with bhi >= mth (hi if none)
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (bhi(mid * kDcKB) >= mth) hi = mid;
+      else lo = mid + 1;
+    }
+    ks0 = lo * kDcKB;
+  }
+  auto need = [&](int i, int bk) { return !cz || bk >= th[i]; };
   const E* qt = (const E*)a.qt + (int64_t)bh * D * Lp;
 
   f32x4 acc[kDcRows][NDT];
@@ -764,22 +808,24 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
     }
   };
   auto load_a = [&](int64_t kb, F (&dst)[kDcRows][KS]) {
+    const int bk = cz ? bhi(kb) : 0;
 #pragma unroll
     for (int i = 0; i < kDcRows; ++i) {
       const int rt = rt0 + 8 * i;
-      if (rt < ntile) {
+      if (rt < ntile && need(i, bk)) {
         const E* ap = gt + (int64_t)(16 * rt + col) * Lp + kb + M::KPL * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) dst[i][ks] = ld_frag(ap + ks * M::K);
       }
     }
   };
-  if (k0 < k1) {
-    load_q(k0);
-    load_a(k0, af);
+  if (ks0 < k1) {
+    load_q(ks0);
+    load_a(ks0, af);
   }
   int buf = 0;
-  for (int64_t kb = k0; kb < k1; kb += kDcKB, buf ^= 1) {
+  for (int64_t kb = ks0; kb < k1; kb += kDcKB, buf ^= 1) {
+    const int bk = cz ? bhi(kb) : 0;
     store_q(buf);
     __syncthreads();
     const bool more = kb + kDcKB < k1;
@@ -794,7 +840,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
       for (int nd = 0; nd < NDT; ++nd) bq[nd] = ld_frag(qs[buf] + (16 * nd + col) * QS + ks * M::K + M::KPL * g);
 #pragma unroll
       for (int i = 0; i < kDcRows; ++i)
-        if (rt0 + 8 * i < ntile)
+        if (rt0 + 8 * i < ntile && need(i, bk))
 #pragma unroll
           for (int nd = 0; nd < NDT; ++nd) acc[i][nd] = M::mma(af[i][ks], bq[nd], acc[i][nd]);
     }
