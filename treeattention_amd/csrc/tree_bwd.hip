@@ -716,7 +716,9 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
 // dC partial of one query split: dsum_part[split][bh][r][:] = sum over the
 // split's queries of G^T[r][q] Q[q][:].  grid (row chunks, qsplit, BH), eight
 // waves; a row chunk is 8 * kDcRows row tiles of 16 summary rows and wave w
-// owns tiles w, w + 8, ... of it for every head dim.  Per block of 32 queries
+// owns tiles w, w + 8, ... of it for every head dim.  Split s takes the query
+// blocks s, s + qsplit, s + 2 qsplit, ..., so under causal masking (late
+// blocks reach more rows) every split gets the same mix.  Per block of queries
 // the Q^T block is staged once in LDS (double-buffered: the next block's
 // global loads are in flight while the current one is multiplied) and every
 // G^T row is read once, straight from global memory into MFMA fragments.
@@ -738,8 +740,9 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
   const int rows = a.geo.NS, ntile = rows / 16;
   const int64_t Lp = a.Lp;
-  const int64_t per = ((Lp / kDcKB + a.qsplit - 1) / a.qsplit) * kDcKB;
-  const int64_t k0 = (int64_t)split * per, k1 = min(Lp, k0 + per);
+  const int64_t nblk = Lp / kDcKB, qs_ = a.qsplit;
+  const int64_t nj = split < nblk ? (nblk - split + qs_ - 1) / qs_ : 0;  // this split's query blocks
+  auto kb_of = [&](int64_t j) { return (j * qs_ + split) * kDcKB; };
   const int rt0 = chunk * 8 * kDcRows + w;
   const E* gt = (const E*)a.gt + (int64_t)bh * rows * Lp;
   // Exact causal mode: tree_dq_kernel writes the G^T row of column c of level
@@ -766,21 +769,21 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
     const int r = 16 * (rt0 + 8 * i);
     th[i] = cz && r < rows ? thr(level_of(r), r) : 0;
   }
-  int64_t ks0 = k0;
-  if (cz && k0 < k1) {
+  int64_t j0 = 0;
+  if (cz && nj > 0) {
     const int r0 = chunk * 8 * kDcRows * 16, r1 = min(rows, r0 + 8 * kDcRows * 16);
     int mth = 0x7fffffff;
     for (int lam = 1; lam <= G.T; ++lam) {
       const int lo = max(r0, G.off[lam]), hi = min(r1, G.off[lam + 1]);
       if (lo < hi) mth = min(mth, thr(lam, lo));
     }
-    int64_t lo = k0 / kDcKB, hi = k1 / kDcKB;  // first block in [lo, hi) with bhi >= mth (hi if none)
+    int64_t lo = 0, hi = nj;  // first j in [0, nj) with bhi >= mth (nj if none)
     while (lo < hi) {
       const int64_t mid = (lo + hi) >> 1;
-      if (bhi(mid * kDcKB) >= mth) hi = mid;
+      if (bhi(kb_of(mid)) >= mth) hi = mid;
       else lo = mid + 1;
     }
-    ks0 = lo * kDcKB;
+    j0 = lo;
   }
   auto need = [&](int i, int bk) { return !cz || bk >= th[i]; };
   const E* qt = (const E*)a.qt + (int64_t)bh * D * Lp;
@@ -819,19 +822,19 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
       }
     }
   };
-  if (ks0 < k1) {
-    load_q(ks0);
-    load_a(ks0, af);
+  if (j0 < nj) {
+    load_q(kb_of(j0));
+    load_a(kb_of(j0), af);
   }
   int buf = 0;
-  for (int64_t kb = ks0; kb < k1; kb += kDcKB, buf ^= 1) {
-    const int bk = cz ? bhi(kb) : 0;
+  for (int64_t j = j0; j < nj; ++j, buf ^= 1) {
+    const int bk = cz ? bhi(kb_of(j)) : 0;
     store_q(buf);
     __syncthreads();
-    const bool more = kb + kDcKB < k1;
+    const bool more = j + 1 < nj;
     if (more) {
-      load_q(kb + kDcKB);
-      load_a(kb + kDcKB, an);
+      load_q(kb_of(j + 1));
+      load_a(kb_of(j + 1), an);
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
