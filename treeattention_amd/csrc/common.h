@@ -520,8 +520,8 @@ struct BwdWorkspaceLayout {
   int64_t dq_part;   // E (B, L, H, S, D): leaf dq per distinct leaf block
   int64_t dlogp;     // float (B, L, H, S): gradient of each distinct leaf block's summed log-prob
   int64_t dk_leaf;   // float (B, N, H, D)
-  int64_t gt;        // E (BH, NS, Lp): gradient of the child logits, transposed (queries contiguous)
-  int64_t qt;        // E (BH, D, Lp): queries transposed
+  int64_t gt;        // E (BH, Lp/64, NS, 64): gradient of the child logits, transposed per 64-query tile
+  int64_t qt;        // E (BH, Lp/64, D, 64): queries transposed per 64-query tile
   int64_t dsum_part; // float (qsplit, BH, NS, D)
   int64_t dsum;      // float (BH, NS, D)
   int64_t rc_coef;   // float (B, L, H, T): reference causal mode, boundary-mass gradient scale

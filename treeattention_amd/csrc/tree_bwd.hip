@@ -13,7 +13,8 @@
 // so the blocks under any node are one contiguous run, summed by segmented
 // scans with one writer per entry of G -- no conflicts, no atomics.  Then
 //   tree_dq_kernel: dq = sum_u dq_pair[u] + sum_chunks G C_chunk (MFMA); it
-//     also writes G^T and Q^T with the queries contiguous;
+//     also writes G^T and Q^T per tile of 64 queries, queries contiguous
+//     (one contiguous block per tile and chunk);
 //   tree_dc_kernel: dC = G^T Q per query split, a plain MFMA product of the
 //     two (no recomputation of logits or G), skipping under exact causal
 //     masking the (row tile, query block) pairs whose G^T rows are all zero;
@@ -46,8 +47,8 @@ struct TreeArgs {
   const float* delta;
   const void* dq_part;
   float* dl;           // (B, L, H, S) per distinct block
-  void* gt;            // E (BH, NS, Lp)
-  void* qt;            // E (BH, D, Lp)
+  void* gt;            // E (BH, Lp / 64, NS, 64): G^T per query tile
+  void* qt;            // E (BH, Lp / 64, D, 64): Q^T per query tile
   int64_t Lp;
   void* dq;
   float* dsum_part;
@@ -507,10 +508,10 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       }
     }
     __syncthreads();
-    E* qt_out = (E*)a.qt + (int64_t)bh * D * a.Lp + l0;
+    E* qt_out = (E*)a.qt + ((int64_t)bh * gridDim.x + blockIdx.x) * D * kQueryTile;  // this tile's [D][64]
     for (int e = tid; e < D * (kQueryTile / 8); e += 256) {
       const int dd = e >> 3, q0 = (e & 7) * 8;
-      cp8(qt_out + (int64_t)dd * a.Lp + q0, qst + dd * kQueryTile + q0);
+      cp8(qt_out + dd * kQueryTile + q0, qst + dd * kQueryTile + q0);
     }
     __syncthreads();
   }
@@ -646,13 +647,13 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       // G^T rows of the chunk up to the reach (without the causal restriction
       // rk covers the chunk rounded up to 32 rows, the level's zero padding
       // included), eight queries per 16-byte store
-      E* gt = (E*)a.gt + ((int64_t)bh * rows + G.off[lam] + c0) * a.Lp + l0;
+      E* gt = (E*)a.gt + (((int64_t)bh * gridDim.x + blockIdx.x) * rows + G.off[lam] + c0) * kQueryTile;
       for (int e = tid; e < rk * (kQueryTile / 8); e += 256) {
         const int cc = e >> 3, q0 = (e & 7) * 8;
         E v8[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v8[i] = sm.Gm[(q0 + i) * kGS + cc];
-        cp8(gt + (int64_t)cc * a.Lp + q0, v8);
+        cp8(gt + cc * kQueryTile + q0, v8);
       }
     }
     // dq^T += C^T G^T: A = C^T rows (head dims, registers), B = G rows (LDS)
@@ -744,7 +745,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   const int64_t nj = split < nblk ? (nblk - split + qs_ - 1) / qs_ : 0;  // this split's query blocks
   auto kb_of = [&](int64_t j) { return (j * qs_ + split) * kDcKB; };
   const int rt0 = chunk * 8 * kDcRows + w;
-  const E* gt = (const E*)a.gt + (int64_t)bh * rows * Lp;
+  const E* gt = (const E*)a.gt + (int64_t)bh * rows * Lp;  // [query block][row][kDcKB]
   // Exact causal mode: tree_dq_kernel writes the G^T row of column c of level
   // lam for a query block only where (c & ~31) is below that block's reach,
   // i.e. where ((c & ~31) >> lb) << lb (T - lam + 1) <= blk_hi, the block's
@@ -786,7 +787,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
     j0 = lo;
   }
   auto need = [&](int i, int bk) { return !cz || bk >= th[i]; };
-  const E* qt = (const E*)a.qt + (int64_t)bh * D * Lp;
+  const E* qt = (const E*)a.qt + (int64_t)bh * D * Lp;    // [query block][D][kDcKB]
 
   f32x4 acc[kDcRows][NDT];
 #pragma unroll
@@ -800,7 +801,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int e = tid + 512 * j;
-      if (e < NLD) cp8(qreg[j], qt + (int64_t)(e / (kDcKB / 8)) * Lp + kb + (e % (kDcKB / 8)) * 8);
+      if (e < NLD) cp8(qreg[j], qt + kb * D + e * 8);
     }
   };
   auto store_q = [&](int buf) {
@@ -816,7 +817,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
     for (int i = 0; i < kDcRows; ++i) {
       const int rt = rt0 + 8 * i;
       if (rt < ntile && need(i, bk)) {
-        const E* ap = gt + (int64_t)(16 * rt + col) * Lp + kb + M::KPL * g;
+        const E* ap = gt + ((kb / kDcKB) * rows + 16 * rt + col) * kDcKB + M::KPL * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) dst[i][ks] = ld_frag(ap + ks * M::K);
       }
