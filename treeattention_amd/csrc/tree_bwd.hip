@@ -882,24 +882,31 @@ __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restric
 }
 
 // dk[b, t, h, :] = dk_leaf + sum over the summaries that include token t.
-// One thread per (token, 4 dims); grid (ceil(N*D/4/256), BH).
+// One thread per (token, 8 dims): one 16-byte store for 16-bit outputs (the
+// entry points require 16-byte aligned dk and strides in multiples of 8);
+// grid (ceil(N*D/8/256), BH).
 template <typename E>
 __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
   const Geo& G = a.geo;
   const int D = a.D;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)a.N * D / 4) return;
+  if (e >= (int64_t)a.N * D / 8) return;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
-  const int t = (int)(e / (D / 4)), d0 = (int)(e - (int64_t)t * (D / 4)) * 4;
+  const int t = (int)(e / (D / 8)), d0 = (int)(e - (int64_t)t * (D / 8)) * 8;
   const int beta = t / G.LB;
   const float* ds = a.dsum + (int64_t)bh * G.NS * D + d0;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  auto add = [&](const float4& x, const float4& y, float s) {
+    acc[0] += x.x * s; acc[1] += x.y * s; acc[2] += x.z * s; acc[3] += x.w * s;
+    acc[4] += y.x * s; acc[5] += y.y * s; acc[6] += y.z * s; acc[7] += y.w * s;
+  };
   if (a.mode == TA_TREE_NATURAL) {
     for (int lam = 1; lam <= G.T; ++lam) {
       const int shift = G.lb * (G.T - lam);  // leaf blocks per node = 2^shift
-      const float4 v = *(const float4*)(ds + (int64_t)(G.off[lam] + (beta >> shift)) * D);
-      const float s = 1.f / (float)(2 << shift);
-      acc[0] += v.x * s; acc[1] += v.y * s; acc[2] += v.z * s; acc[3] += v.w * s;
+      const float4* v = (const float4*)(ds + (int64_t)(G.off[lam] + (beta >> shift)) * D);
+      add(v[0], v[1], 1.f / (float)(2 << shift));
     }
   } else {
     // compat: dcoef_n = (dC_left - dC_right)/2 for heap node n; the in-order
@@ -911,19 +918,31 @@ __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
       const int dep = 31 - __clz(nn + 1);
       const int ip = nn + 1 - (1 << dep);
       const int64_t rl = G.off[dep + 1] + 2 * ip;
-      const float4 x = *(const float4*)(ds + rl * D), y = *(const float4*)(ds + (rl + 1) * D);
+      const float4* x = (const float4*)(ds + rl * D);
+      const float4* y = (const float4*)(ds + (rl + 1) * D);
+      const float4 x0 = x[0], x1 = x[1], y0 = y[0], y1 = y[1];
       const float s = (beta < p ? 0.25f : -0.25f) / (float)wl;
-      acc[0] += (x.x - y.x) * s; acc[1] += (x.y - y.y) * s; acc[2] += (x.z - y.z) * s; acc[3] += (x.w - y.w) * s;
+      add(make_float4(x0.x - y0.x, x0.y - y0.y, x0.z - y0.z, x0.w - y0.w),
+          make_float4(x1.x - y1.x, x1.y - y1.y, x1.z - y1.z, x1.w - y1.w), s);
     }
   }
   const float inv = 1.f / (float)G.LB;
   const int64_t th = ((int64_t)bb * a.N + t) * a.H + h;
-  const float4 lk = *(const float4*)(a.dk_leaf + th * D + d0);
+  const float4* lk = (const float4*)(a.dk_leaf + th * D + d0);
+  const float4 l0 = lk[0], l1 = lk[1];
+  const float r[8] = {l0.x + acc[0] * inv, l0.y + acc[1] * inv, l0.z + acc[2] * inv, l0.w + acc[3] * inv,
+                      l1.x + acc[4] * inv, l1.y + acc[5] * inv, l1.z + acc[6] * inv, l1.w + acc[7] * inv};
   E* o = (E*)a.dk + bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d0;
-  o[0] = (E)(lk.x + acc[0] * inv);
-  o[1] = (E)(lk.y + acc[1] * inv);
-  o[2] = (E)(lk.z + acc[2] * inv);
-  o[3] = (E)(lk.w + acc[3] * inv);
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(8))) E e8;
+    e8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (E)r[i];
+    *(e8*)o = v;
+  } else {
+    *(float4*)o = make_float4(r[0], r[1], r[2], r[3]);
+    *(float4*)(o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+  }
 }
 
 // Node-keys mode: dk[node n] = (dC_left - dC_right) / 2.
@@ -1027,7 +1046,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     if (n > 0)
       hipLaunchKernelGGL(nodekeys_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
   } else {
-    const int64_t n = P.N * D / 4;
+    const int64_t n = P.N * D / 8;
     hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
   }
   return hipGetLastError();
