@@ -65,11 +65,19 @@ def _node_dots(q_lbhd: torch.Tensor, k: torch.Tensor, nodes: torch.Tensor) -> to
     return (q_lbhd.unsqueeze(-2) * kg).sum(-1)
 
 
-def sample_non_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U):
+def _forced_dirs(forced, d: int, T: int):
+    """Direction at depth ``d`` of the given leaves: bit ``T-1-d`` (``node <- 2 node + 1 + dir``)."""
+    return (torch.as_tensor(np.asarray(forced), dtype=torch.long) >> (T - 1 - d)) & 1
+
+
+def sample_non_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U, forced=None):
     """``_sample_paths_non_causal`` (``_tree_mha.py:78-122``).
 
     ``q`` (L, B, H, D), ``k`` (K, B, H, D); ``U`` (B, L, H, S, T, 2).
     Returns ``idx`` (L, B, H, S), differentiable ``lp`` and per-decision margins.
+    ``forced`` (L, B, H, S) leaf ids: take these paths instead of the
+    Gumbel-max decisions (the log-probs and margins are those of the forced
+    paths), to evaluate the op on paths another implementation sampled.
     """
     L, B, H, _ = q.shape
     K = num_leaves - 1
@@ -84,7 +92,7 @@ def sample_non_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U):
         x = _node_dots(q, k, nodes)
         lp = torch.stack([F.logsigmoid(x), F.logsigmoid(-x)], dim=-1)
         score = lp.detach() + g[..., d, :]
-        dirs = _first_argmax(score)
+        dirs = _first_argmax(score) if forced is None else _forced_dirs(forced, d, T)
         margins[..., d] = _margin(score)
         chosen = torch.gather(lp, -1, dirs.unsqueeze(-1)).squeeze(-1)
         acc = acc + torch.where(valid, chosen, torch.full_like(chosen, _NEG_INF))
@@ -92,7 +100,7 @@ def sample_non_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U):
     return nodes - K, acc, margins
 
 
-def sample_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U, offset: int = 0):
+def sample_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U, offset: int = 0, forced=None):
     """``_sample_paths_causal`` (``_tree_mha.py:125-268``).
 
     ``q`` (L', B, H, D) are the queries at absolute positions
@@ -100,7 +108,9 @@ def sample_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U, offset: 
     absolute position.  Returns ``idx`` (L', B, H, S), differentiable ``lp``,
     margins and ``dstar`` (L',): the first depth at which not every lane of
     the query sits on the boundary path (``T`` if none), i.e. where the
-    reference stops correcting.
+    reference stops correcting.  ``forced`` (L', B, H, S) leaf ids: take these
+    paths instead of the Gumbel-max decisions; the corrections still follow
+    the reference's rule for the nodes the forced paths visit.
     """
     Lq, B, H, _ = q.shape
     K = num_leaves - 1
@@ -157,7 +167,7 @@ def sample_causal(q: torch.Tensor, k: torch.Tensor, num_leaves: int, U, offset: 
                 lpr = mr + lpr - mparent
             lp = torch.stack([lpl, lpr], dim=-1)
             score = lp.detach() + g[:, c, :, :, d, :]
-            dirs = _first_argmax(score)
+            dirs = _first_argmax(score) if forced is None else _forced_dirs(np.asarray(forced)[t], d, T)
             margins[t, ..., d] = _margin(score)
             acc = acc + torch.gather(lp, -1, dirs.unsqueeze(-1)).squeeze(-1)
             nodes = 2 * nodes + 1 + dirs
@@ -200,14 +210,16 @@ def deterministic_attention(q, k, v, is_causal: bool):
 
 
 def hierarchical_attention(query, key, value, num_heads: int, is_causal: bool = False,
-                           mode: str = "stochastic", num_samples: int = 64, U=None):
+                           mode: str = "stochastic", num_samples: int = 64, U=None, forced=None):
     """``hierarchical_attention`` (``_tree_mha.py:324-413``) on float64 tensors.
 
     ``query`` (L, B, E), ``key`` (N-1, B, E), ``value`` (N, B, E); ``U`` the
     uniforms (B, L, H, S, T, 2) for stochastic mode.  Returns ``(out (L, B, E),
     weights)`` with the reference's shapes (hybrid causal: weights of the
     stochastic rows only) and, for stochastic mode, a dict with ``idx``,
-    ``margins`` and ``dstar`` of the sampled rows.
+    ``margins`` and ``dstar`` of the sampled rows.  ``forced``: leaf ids of
+    the sampled rows (``(L - S, B, H, S)`` for the causal hybrid, else
+    ``(L, B, H, S)``) to evaluate on instead of sampling.
     """
     L, B, E = query.shape
     N = value.shape[0]
@@ -225,14 +237,14 @@ def hierarchical_attention(query, key, value, num_heads: int, is_causal: bool = 
     hybrid = is_causal and L > S
     if hybrid:
         out_det, _ = deterministic_attention(q[:S], k, v, True)
-        idx, lp, margins, dstar = sample_causal(q[S:], k, N, U, offset=S)
+        idx, lp, margins, dstar = sample_causal(q[S:], k, N, U, offset=S, forced=forced)
         info["dstar"] = dstar
     elif is_causal:
-        idx, lp, margins, dstar = sample_causal(q, k, N, U, offset=0)
+        idx, lp, margins, dstar = sample_causal(q, k, N, U, offset=0, forced=forced)
         info["dstar"] = dstar
     else:
-        idx, lp, margins = sample_non_causal(q, k, N, U)
-    info.update(idx=idx, margins=margins)
+        idx, lp, margins = sample_non_causal(q, k, N, U, forced=forced)
+    info.update(idx=idx, margins=margins, lp=lp.detach())
     valid = (idx >= 0) & (idx < N)
     lp = lp.masked_fill(~valid, _NEG_INF)
     w = torch.softmax(lp, dim=-1)

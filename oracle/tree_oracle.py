@@ -607,6 +607,91 @@ def tree_backward(q, k, v, C, branching, leaf_block, idx, w, dout, causal, scale
     return dq, dC, dk, dv
 
 
+def head_fwd_bwd(q, k, v, dout, C, branching, leaf_block, idx, causal, scale, max_logit=1e3):
+    """``tree_forward`` + ``tree_backward`` of ONE (batch, head) on given paths,
+    organized by leaf block so that full-size heads run in seconds.
+
+    Same mathematics as ``leaf_attention`` / ``sample_weights(path_logprobs)``
+    / ``tree_backward`` (``_tree_mha.py:396-407``, ``_autograd.py:744-858``),
+    but every (query, sample) pair of a leaf block is processed as one matrix
+    product against that block's keys and values, and the child-logit
+    gradient is a dense ``(L, NS)`` matrix ``G`` with ``dq += G C`` and
+    ``dC = G^T q``.  Pinned against those functions in
+    ``tests/test_oracle.py::test_head_fwd_bwd_matches_explicit``.
+
+    ``q``, ``dout`` (L, D); ``k``, ``v`` (N, D); ``C`` (NS, D) child summaries;
+    ``idx`` (L, S) leaf blocks.  Returns a dict with ``out`` (L, D),
+    ``weights`` (L, S), ``dq`` (L, D), ``dC`` (NS, D), ``dk_leaf``, ``dv`` (N, D).
+    """
+    q64, k64, v64, g64, C64 = (np.asarray(x, dtype=np.float64) for x in (q, k, v, dout, C))
+    L, D = q64.shape
+    N = v64.shape[0]
+    S = idx.shape[1]
+    b, LB = branching, leaf_block
+    nl = N // LB
+    T = tree_depth(nl, b)
+    off = level_offsets(b, T)
+    lp = path_logprobs(q64[None, :, None], C64[None, None], b, nl, idx[None, :, None], max_logit)[0, :, 0]
+    w = sample_weights(lp)
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    starts = np.searchsorted(flat[order], np.arange(nl + 1))
+    pos = np.arange(L) + (N - L)
+
+    def block_pairs(beta):
+        pr = order[starts[beta]:starts[beta + 1]]
+        l_p, s_p = pr // S, pr % S
+        Kb, Vb = k64[beta * LB:(beta + 1) * LB], v64[beta * LB:(beta + 1) * LB]
+        z = scale * (q64[l_p] @ Kb.T)
+        if causal:
+            z = np.where(beta * LB + np.arange(LB)[None, :] > pos[l_p][:, None], -np.inf, z)
+        z = z - z.max(axis=1, keepdims=True)
+        a = np.exp(z)
+        a /= a.sum(axis=1, keepdims=True)
+        return l_p, s_p, Kb, Vb, a
+
+    o_pair = np.zeros((L, S, D))
+    for beta in range(nl):
+        l_p, s_p, _, Vb, a = block_pairs(beta)
+        o_pair[l_p, s_p] = a @ Vb
+    out = np.einsum("ls,lsd->ld", w, o_pair)
+    delta = np.einsum("ld,lsd->ls", g64, o_pair)
+    dlp = w * (delta - (w * delta).sum(axis=1, keepdims=True))
+
+    dq_pair = np.zeros((L, S, D))
+    dk = np.zeros((N, D))
+    dv = np.zeros((N, D))
+    for beta in range(nl):
+        l_p, s_p, Kb, Vb, a = block_pairs(beta)
+        ws = w[l_p, s_p]
+        Gl = g64[l_p]
+        dz = a * (ws[:, None] * (Gl @ Vb.T) - (ws * delta[l_p, s_p])[:, None])
+        dq_pair[l_p, s_p] = scale * (dz @ Kb)
+        dk[beta * LB:(beta + 1) * LB] = scale * (dz.T @ q64[l_p])
+        dv[beta * LB:(beta + 1) * LB] = (a * ws[:, None]).T @ Gl
+    dq = dq_pair.sum(axis=1)
+
+    half = max_logit / 2
+    Xr = q64 @ C64.T
+    X = np.clip(Xr, -half, half)
+    live = (Xr >= -half) & (Xr <= half)
+    G = np.zeros_like(X)
+    jj = np.arange(b)
+    rows = np.broadcast_to(np.arange(L)[:, None, None], (L, S, b))
+    for d in range(T):
+        node = idx // b ** (T - d)
+        jstar = (idx // b ** (T - 1 - d)) % b
+        cols = off[d + 1] + b * node[..., None] + jj  # (L, S, b)
+        x = np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+        p = np.exp(x - _lse(x)[..., None])
+        lv = np.take_along_axis(live, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+        dx = dlp[..., None] * ((jj == jstar[..., None]) - p) * lv
+        np.add.at(G, (rows.reshape(-1), cols.reshape(-1)), dx.reshape(-1))
+    dq += G @ C64
+    dC = G.T @ q64
+    return dict(out=out, weights=w, lp=lp, dq=dq, dC=dC, dk_leaf=dk, dv=dv)
+
+
 def summaries(k, branching, leaf_block, tree_mode):
     """Child summaries for ``tree_mode`` in {"natural", "compat"}."""
     if tree_mode == "natural":

@@ -75,13 +75,19 @@ def test_gpu_matches_reference_fixture(path):
     clean = info["margins"].numpy().min(axis=-1) > (5e-2 if bf16 else 1e-3)
     got = leaves[t0:]
     np.testing.assert_array_equal(got[clean], fx["idx"][clean])
+    ref = dict(out=fx["out"], weights=fx["weights"], dq=fx["dq"], dk=fx["dk"], dv=fx["dv"])
     if not (got == fx["idx"]).all():
-        assert bf16, "float32: a decision flipped"
-        pytest.skip("bfloat16 near-tie took the other branch; clear decisions checked")
-    assert rel(out.reshape(L, B, H * D), fx["out"]) < tol
-    assert rel(w[t0:], fx["weights"]) < tol
-    for got_g, ref in ((dq, fx["dq"]), (dk, fx["dk"]), (dv, fx["dv"])):
-        assert rel(got_g.reshape(ref.shape), ref) < tol
+        # a near-tie went the other way: compare with the float64 restatement (pinned to
+        # this very fixture by tests/test_golden.py) evaluated on the GPU's own paths
+        print(f"  {int((got != fx['idx']).sum())} near-tie samples differ; oracle on the GPU's paths", flush=True)
+        o_out, o_w, _, o_dq, o_dk, o_dv = _oracle_run(fx["q"], fx["k"], fx["v"], fx["dout"].reshape(L, B, H, D),
+                                                      fx["U"], S, causal, forced=got)
+        ref = dict(out=o_out.reshape(L, B, H * D), weights=o_w, dq=o_dq, dk=o_dk, dv=o_dv)
+    assert rel(out.reshape(L, B, H * D), ref["out"]) < tol
+    assert rel(w[t0:], ref["weights"]) < tol
+    for name in ("dq", "dk", "dv"):
+        g = {"dq": dq, "dk": dk, "dv": dv}[name]
+        assert rel(g.reshape(ref[name].shape), ref[name]) < tol, name
 
 
 def test_op_level_weights_shape_follows_reference_hybrid():
@@ -95,11 +101,13 @@ def test_op_level_weights_shape_follows_reference_hybrid():
     assert w.shape == (S, B, H, S)
 
 
-def _oracle_run(q, k, v, dout, U, S, causal):
+def _oracle_run(q, k, v, dout, U, S, causal, forced=None):
+    """The float64 restatement with autograd; ``forced``: leaf ids of the sampled rows to
+    evaluate on instead of sampling."""
     L, B, H, D = q.shape
-    qt, kt, vt = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v))
+    qt, kt, vt = (torch.tensor(np.asarray(x), dtype=torch.float64, requires_grad=True) for x in (q, k, v))
     out, w, info = R.hierarchical_attention(qt.reshape(L, B, H * D), kt.reshape(L - 1, B, H * D),
-                                            vt.reshape(L, B, H * D), H, causal, "stochastic", S, U)
+                                            vt.reshape(L, B, H * D), H, causal, "stochastic", S, U, forced=forced)
     out.backward(torch.tensor(dout, dtype=torch.float64).reshape(L, B, H * D))
     return (out.detach().numpy().reshape(L, B, H, D), w.detach().numpy(), info, qt.grad.numpy(), kt.grad.numpy(),
             vt.grad.numpy())
@@ -129,7 +137,8 @@ def test_gpu_reference_causal_against_restatement(L, B, H, D, S, dtype):
     if t0:
         assert (info["dstar"] < T).any() and (leaves[t0:] > np.arange(t0, L)[:, None, None, None]).any()
     if not (leaves[t0:] == idx_o).all():
-        pytest.skip("a near-tie decision took the other branch; clear decisions checked")
+        print(f"  {int((leaves[t0:] != idx_o).sum())} near-tie samples differ; oracle on the GPU's paths", flush=True)
+        out_o, w_o, info, dq_o, dk_o, dv_o = _oracle_run(q, k, v, do, U, S, True, forced=leaves[t0:])
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
     assert rel(out, out_o) < tol
     assert rel(w[t0:], w_o) < max(tol, 1e-5)
@@ -163,7 +172,14 @@ def test_adapter_reference_tree_causal_matches_restatement():
     clean = info["margins"].numpy().min(axis=-1) > 1e-3
     np.testing.assert_array_equal(leaves[S:][clean], info["idx"].numpy()[clean])
     if not (leaves[S:] == info["idx"].numpy()).all():
-        pytest.skip("a near-tie decision took the other branch; clear decisions checked")
+        print(f"  {int((leaves[S:] != info['idx'].numpy()).sum())} near-tie samples differ; oracle on the GPU's "
+              "paths", flush=True)
+        for t in (kn, qt, vt):
+            t.grad = None
+        out_o, _, info = R.hierarchical_attention(qt.reshape(L, B, H * D), kn.reshape(L - 1, B, H * D),
+                                                  vt.reshape(L, B, H * D), H, True, "stochastic", S,
+                                                  U.cpu().numpy(), forced=leaves[S:])
+        out_o.backward(torch.tensor(do.double().numpy().transpose(1, 0, 2, 3)).reshape(L, B, H * D))
     assert rel(f64(out).transpose(1, 0, 2, 3), out_o.detach().numpy().reshape(L, B, H, D)) < 1e-5
     dk_o = O.haar_inorder_adjoint(kn.grad.numpy())  # (L, B, H, D)
     assert rel(f64(dq).transpose(1, 0, 2, 3), qt.grad.numpy()) < 1e-5

@@ -356,3 +356,85 @@ def test_backward_finite_differences_reference_mode():
                 return np.sum(r["out"] * g)
             fd = (loss(xp) - loss(xm)) / (2 * eps)
             assert abs(fd - base[name][i]) < 1e-6 * max(1, abs(fd)), (name, i, fd, base[name][i])
+
+
+# ------------------------------------------------------- path log-probs ----
+
+
+@pytest.mark.parametrize("b", [2, 4, 8])
+@pytest.mark.parametrize("LB", [1, 3])
+def test_path_logprobs_pinned(b, LB):
+    """``path_logprobs`` (``_tree_mha.py:112-117``: the chosen child's log-prob
+    summed along the path) three ways: against brute-force enumeration of every
+    leaf block's path, against the sampler's own accumulated log-probs
+    (non-causal), and against the exact causal sampler's corrected log-probs
+    plus ``log A_root`` (the allowed mass), with N != L."""
+    rng = np.random.default_rng(100 + 10 * b + LB)
+    T = 2 if b == 8 else 3
+    nl = b**T
+    N = LB * nl
+    B, H, D, S = 2, 2, 4, 6
+    mode = "compat" if b == 2 and LB == 3 else "natural"
+    k = 1.5 * rng.standard_normal((B, N, H, D))
+    C = O.summaries(k, b, LB, mode)
+    # (1) brute force on random leaf blocks
+    L = 5
+    q = rng.standard_normal((B, L, H, D))
+    idx = rng.integers(0, nl, size=(B, L, H, S))
+    lp = O.path_logprobs(q, C, b, nl, idx)
+    for bb in range(B):
+        for h in range(H):
+            for l in range(L):
+                exact = _leaf_logprobs_bary(q[bb, l, h], C[bb, h], b, T)
+                assert abs(np.logaddexp.reduce(exact)) < 1e-12
+                np.testing.assert_allclose(lp[bb, l, h], exact[idx[bb, l, h]], rtol=1e-12, atol=1e-12)
+    # (2) the non-causal sampler's accumulated log-probs
+    U = O.uniforms(7, (B, L, H, S, T, b))
+    idx_s, lp_s, _ = O.tree_sample(q, C, b, LB, U, causal=False, N=N)
+    np.testing.assert_allclose(O.path_logprobs(q, C, b, nl, idx_s), lp_s, rtol=1e-12, atol=1e-12)
+    # (3) exact causal mode, L < N (bottom-right aligned): lp_sampler + log A_root = path log-prob
+    Lc = N - 2 * LB - 1
+    qc = rng.standard_normal((B, Lc, H, D))
+    Uc = O.uniforms(8, (B, Lc, H, S, T, b))
+    idx_c, lp_c, _ = O.tree_sample(qc, C, b, LB, Uc, causal=True, N=N)
+    full = O.path_logprobs(qc, C, b, nl, idx_c)
+    for bb in range(B):
+        for h in range(H):
+            for l in (0, Lc // 2, Lc - 1):
+                blk = (l + N - Lc) // LB
+                assert idx_c[bb, l, h].max() <= blk
+                exact = _leaf_logprobs_bary(qc[bb, l, h], C[bb, h], b, T)
+                logA = np.logaddexp.reduce(exact[:blk + 1])
+                np.testing.assert_allclose(lp_c[bb, l, h] + logA, full[bb, l, h], rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("b,LB,causal,mode,NmL", [
+    (2, 1, False, "compat", 0), (2, 4, True, "compat", 8), (4, 2, False, "natural", 0),
+    (4, 4, True, "natural", 0), (2, 3, True, "natural", 5),
+])
+def test_head_fwd_bwd_matches_explicit(b, LB, causal, mode, NmL):
+    """The per-head, block-organized ``head_fwd_bwd`` against ``leaf_attention``,
+    ``path_logprobs`` / ``sample_weights`` and ``tree_backward`` (each pinned
+    above) on the same paths, every output and gradient."""
+    rng = np.random.default_rng(21)
+    H, D, S = 2, 8, 5
+    nl = b**3
+    N = LB * nl
+    L = N - NmL
+    q, g = (rng.standard_normal((1, L, H, D)) for _ in range(2))
+    k, v = (rng.standard_normal((1, N, H, D)) for _ in range(2))
+    U = O.uniforms(4, (1, L, H, S, 3, b))
+    C = O.summaries(k, b, LB, mode)
+    idx, _, _ = O.tree_sample(q, C, b, LB, U, causal, N=N)
+    w = O.sample_weights(O.path_logprobs(q, C, b, nl, idx))
+    o_s, _ = O.leaf_attention(q, k, v, idx, LB, causal, 0.3)
+    out = np.einsum("blhs,blhsd->blhd", w, o_s)
+    dq, dC, dkl, dv = O.tree_backward(q, k, v, C, b, LB, idx, w, g, causal, 0.3)
+    for h in range(H):
+        r = O.head_fwd_bwd(q[0, :, h], k[0, :, h], v[0, :, h], g[0, :, h], C[0, h], b, LB, idx[0, :, h], causal, 0.3)
+        np.testing.assert_allclose(r["weights"], w[0, :, h], rtol=1e-12, atol=1e-14)
+        np.testing.assert_allclose(r["out"], out[0, :, h], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(r["dq"], dq[0, :, h], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(r["dC"], dC[0, h], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(r["dk_leaf"], dkl[0, :, h], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(r["dv"], dv[0, :, h], rtol=1e-10, atol=1e-12)
