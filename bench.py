@@ -101,34 +101,77 @@ def read_traffic(phase: str, config: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(cfg) -> dict:
-    """The float64 numpy oracle, 1 thread, on the last `nq` queries of one (batch, head)."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+# Queries timed per config by the CPU baseline (all heads of batch element 0, the
+# last CPU_QUERIES[c] positions, against the full-length tree, keys and values).
+CPU_QUERIES = {"C1": 1024, "C2": 512, "C3": 128, "C4": 64, "C5-D32": 512, "C5-D96": 256}
 
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Every host core this process may use (its affinity set), capped by the
+    OMP_NUM_THREADS share the host gives it when that is set."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() else n
+
+
+def cpu_baseline(name: str, cfg) -> dict:
+    """The reference's CPU path (``oracle/cpu_path.py``: torch float32, the
+    reference's op order -- per-depth gathers, query-block streaming, the
+    explicit streaming backward) on every host core: 1 warmup, then the median
+    of 3 of the forward and of the whole step, on a bounded sample of the
+    workload (all heads of batch 0, the last ``CPU_QUERIES`` positions, full
+    tree)."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_path as P
     from oracle import tree_oracle as O
 
     B, L, H, D, dt, b, LB, S, causal, kind = cfg
-    nq = 2048 if L >= 4096 else L
-    rng = np.random.default_rng(0)
-    q = rng.standard_normal((1, nq, 1, D)).astype(np.float32)
-    k = rng.standard_normal((1, L, 1, D)).astype(np.float32)
-    v = rng.standard_normal((1, L, 1, D)).astype(np.float32)
-    do = rng.standard_normal((1, nq, 1, D)).astype(np.float32)
-    T = round(math.log(L // LB, b))
-    U = O.uniforms(0, (1, nq, 1, S, T, b))
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    nq = min(L, CPU_QUERIES[name])
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(L, H, D, generator=g) for _ in range(3))
+    do = torch.randn(nq, H, D, generator=g)
+    if kind == "scaled":
+        q, k, v = (x / math.sqrt(D) for x in (q, k, v))
+    T = O.tree_depth(L // LB, b)
+    per_q = H * S * T * b  # uniforms per position of the (B, L, H, S, T, b) tensor; batch 0
+    flat = (L - nq) * per_q + np.arange(nq * per_q)
+    U = torch.from_numpy(O.uniforms_at(0, flat).reshape(nq, H, S, T, b))
     mode = "natural" if b != 2 else "compat"
-    with threadpool_limits(limits=1):
+    prob = P.Problem(q[L - nq:], k, v, U, torch.arange(L - nq, L), b, LB, causal, mode)
+    fwd_s, step_s = [], []
+    for it in range(4):  # 1 warmup + 3 timed
         t0 = time.perf_counter()
-        C = O.summaries(k.astype(np.float64), b, LB, mode)
-        out, w, idx, lp, _ = O.tree_forward(q, k, v, C, b, LB, U, causal)
-        dq, dC, dkl, dv = O.tree_backward(q, k, v, C, b, LB, idx, w, do, causal)
-        dk = dkl + O.pool_adjoint(dC, L, b, LB, mode)
-        dt_s = time.perf_counter() - t0
-    qps = nq / H / dt_s  # one query = all H heads
-    return {"value": qps, "unit": "queries/s", "cores": 1, "kind": "port",
-            "sample": f"numpy float64 oracle fwd+bwd, 1 thread, batch 0 head 0, last {nq} of {L} queries "
-                      f"(full {L}-token tree), {dt_s:.2f} s; scaled by 1/H to whole-query units"}
+        C = P.summaries(prob.k, b, LB, mode)
+        idx, w, out = prob.forward(C)
+        t1 = time.perf_counter()
+        prob.backward(C, idx, w, do)
+        t2 = time.perf_counter()
+        if it:
+            fwd_s.append(t1 - t0)
+            step_s.append(t2 - t0)
+    fwd_m, step_m = sorted(fwd_s)[1], sorted(step_s)[1]
+    frac = nq / (B * L)
+    return {"value": round(nq / step_m, 3), "unit": "queries/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "fwd_ms": round(fwd_m * 1e3, 1), "bwd_ms": round((step_m - fwd_m) * 1e3, 1),
+            "fraction_of_workload": frac,
+            "sample": f"oracle/cpu_path.py (torch float32, the reference's op order: per-depth summary gathers, "
+                      f"per-(query, sample) leaf-block gathers, explicit streaming backward) on {threads} threads; "
+                      f"batch 0, all {H} heads, the last {nq} of {L} queries against the full {L}-token tree "
+                      f"({frac:.2%} of the step's queries); 1 warmup + median of 3; step {step_m:.2f} s"}
 
 
 def det_main(args) -> int:
@@ -371,7 +414,7 @@ def main() -> int:
     copy_gbs = 2 * src.numel() * src.element_size() / (copy_ms / 1e3) / 1e9
     del src, dst
 
-    cpu = None if args.no_cpu else cpu_baseline(cfg)
+    cpu = None if args.no_cpu else cpu_baseline(args.config, cfg)
     step_ms = res["step_ms"]
     line = {
         "metric": "tree-attn fwd+bwd ms & queries/s at L=16k bf16; achieved HBM GB/s %peak",

@@ -91,7 +91,7 @@ def uniforms(seed: int, shape: tuple[int, ...]) -> np.ndarray:
 
     Element with flat (row-major) index ``i`` takes word ``i % 4`` of
     ``philox4x32_10(ctr=(lo(i//4), hi(i//4), 0, 0), key=(lo(seed), hi(seed)))``
-    and maps it to ``((x >> 8) + 0.5) * 2**-24`` (exact in float32).
+    and maps it with ``word_uniform``.
     """
     n = int(np.prod(shape)) if len(shape) else 1
     nblk = (n + 3) // 4
@@ -101,8 +101,27 @@ def uniforms(seed: int, shape: tuple[int, ...]) -> np.ndarray:
     ctr[:, 1] = (idx >> np.uint64(32)).astype(np.uint32)
     key = np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], dtype=np.uint32)
     words = philox4x32_10(ctr, key).reshape(-1)[:n]
-    u = ((words >> np.uint32(8)).astype(np.float64) + 0.5) * (2.0 ** -24)
-    return u.astype(np.float32).reshape(shape)
+    return word_uniform(words).reshape(shape)
+
+
+def uniforms_at(seed: int, flat: np.ndarray) -> np.ndarray:
+    """The elements of ``uniforms(seed, shape)`` at the given flat (row-major)
+    indices, without generating the rest."""
+    flat = np.asarray(flat).astype(np.uint64).reshape(-1)
+    blk = flat >> np.uint64(2)
+    ctr = np.zeros((flat.size, 4), dtype=np.uint32)
+    ctr[:, 0] = (blk & _MASK32).astype(np.uint32)
+    ctr[:, 1] = (blk >> np.uint64(32)).astype(np.uint32)
+    key = np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], dtype=np.uint32)
+    words = philox4x32_10(ctr, key)[np.arange(flat.size), (flat & np.uint64(3)).astype(np.int64)]
+    return word_uniform(words)
+
+
+def word_uniform(words: np.ndarray) -> np.ndarray:
+    """32-bit words -> float32 uniforms ``((x >> 9) + 0.5) * 2**-23``: every value
+    is exact in float32 and lies in ``[2**-24, 1 - 2**-24]``, strictly inside (0, 1)."""
+    u = ((np.asarray(words, dtype=np.uint32) >> np.uint32(9)).astype(np.float64) + 0.5) * (2.0 ** -23)
+    return u.astype(np.float32)
 
 
 def gumbel(u: np.ndarray) -> np.ndarray:

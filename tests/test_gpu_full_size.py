@@ -54,16 +54,7 @@ def inputs(B, L, H, D, dtype, kind):
     return [x.to(dtype) for x in (q, k, v, do)]
 
 
-def uniforms_at(seed: int, flat: np.ndarray) -> np.ndarray:
-    """The generator's uniforms at the given flat indices of the (B, L, H, S, T, b) tensor."""
-    flat = flat.astype(np.uint64)
-    blk = flat >> np.uint64(2)
-    ctr = np.zeros((flat.size, 4), dtype=np.uint32)
-    ctr[:, 0] = (blk & np.uint64(0xFFFFFFFF)).astype(np.uint32)
-    ctr[:, 1] = (blk >> np.uint64(32)).astype(np.uint32)
-    key = np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], dtype=np.uint32)
-    words = O.philox4x32_10(ctr, key)[np.arange(flat.size), (flat & np.uint64(3)).astype(np.int64)]
-    return (((words >> np.uint32(8)).astype(np.float64) + 0.5) * 2.0**-24).astype(np.float32)
+uniforms_at = O.uniforms_at  # the generator's uniforms at flat indices of the (B, L, H, S, T, b) tensor
 
 
 def rel(x, y):

@@ -45,6 +45,11 @@ def test_uniforms_open_interval_and_layout():
     big = O.uniforms(7, (200000,)).astype(np.float64)
     assert abs(big.mean() - 0.5) < 5 * math.sqrt(1 / 12 / big.size)
     assert abs(big.var() - 1 / 12) < 0.002
+    # the extreme words map strictly inside (0, 1) in float32 (so -log(-log u) is finite)
+    ext = O.word_uniform(np.array([0, 1, 0x1FF, 0x200, 0xFFFFFDFF, 0xFFFFFE00, 0xFFFFFFFF], dtype=np.uint32))
+    assert ext[0] == np.float32(2.0**-24) and ext[-1] == np.float32(1 - 2.0**-24) and ext[-1] < 1
+    assert ext[2] == ext[0] and ext[3] == np.float32(1.5 * 2.0**-23) and ext[-2] == ext[-1] and ext[-3] < ext[-2]
+    assert np.isfinite(O.gumbel(ext)).all()
 
 
 # ------------------------------------------------------------------ Haar ----
@@ -438,3 +443,9 @@ def test_head_fwd_bwd_matches_explicit(b, LB, causal, mode, NmL):
         np.testing.assert_allclose(r["dC"], dC[0, h], rtol=1e-10, atol=1e-12)
         np.testing.assert_allclose(r["dk_leaf"], dkl[0, :, h], rtol=1e-10, atol=1e-12)
         np.testing.assert_allclose(r["dv"], dv[0, :, h], rtol=1e-10, atol=1e-12)
+
+
+def test_uniforms_at_matches_full_tensor():
+    u = O.uniforms(9, (3, 7, 5))
+    flat = np.array([0, 1, 2, 3, 4, 17, 50, 101, 104])
+    np.testing.assert_array_equal(O.uniforms_at(9, flat), u.reshape(-1)[flat])

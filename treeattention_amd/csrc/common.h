@@ -448,7 +448,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // -------------------------------------------------------------- counter RNG ---
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).  Uniform i of a tensor is
 // word i%4 of philox(ctr = (lo(i/4), hi(i/4), 0, 0), key = seed), mapped to
-// ((x >> 8) + 0.5) * 2^-24 in (0,1).
+// ((x >> 9) + 0.5) * 2^-23, exact in float32 and inside [2^-24, 1 - 2^-24].
 
 struct Philox4 { uint32_t w[4]; };
 
@@ -483,7 +483,7 @@ __device__ __forceinline__ uint32_t leaf_path_word(uint32_t id, int nbits) {
 }
 
 __device__ __host__ inline float word_to_uniform(uint32_t x) {
-  return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f);
+  return ((float)(x >> 9) + 0.5f) * (1.0f / 8388608.0f);
 }
 
 // ---------------------------------------------------------- record layout ---
