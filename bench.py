@@ -103,7 +103,7 @@ def read_traffic(phase: str, config: str):
 
 # Queries timed per config by the CPU baseline (all heads of batch element 0, the
 # last CPU_QUERIES[c] positions, against the full-length tree, keys and values).
-CPU_QUERIES = {"C1": 1024, "C2": 512, "C3": 128, "C4": 64, "C5-D32": 512, "C5-D96": 256}
+CPU_QUERIES = {"C1": 1024, "C2": 1024, "C3": 512, "C4": 128, "C5-D32": 1024, "C5-D96": 512}
 
 
 def cpu_model() -> str:

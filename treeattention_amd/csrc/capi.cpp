@@ -8,11 +8,9 @@
 #include "launch.h"
 
 namespace ta {
-namespace {
 
 thread_local std::string g_err;
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -28,6 +26,10 @@ int ok() {
   return TA_OK;
 }
 
+const char* last_error() { return g_err.c_str(); }
+
+namespace {
+
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 int64_t align32(int64_t x) { return (x + 31) & ~(int64_t)31; }
 
@@ -41,6 +43,8 @@ struct Carver {
 };
 
 bool strides_ok(const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+
+}  // namespace
 
 // Builds and validates the plan; returns TA_OK or an error code (message set).
 int make_plan(const ta_problem* p, Plan* P) {
@@ -174,6 +178,8 @@ int make_plan(const ta_problem* p, Plan* P) {
   return TA_OK;
 }
 
+namespace {
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int launch_status(hipError_t e, const char* what) {
@@ -190,7 +196,7 @@ extern "C" {
 
 int ta_version(void) { return TA_VERSION; }
 
-const char* ta_last_error(void) { return g_err.c_str(); }
+const char* ta_last_error(void) { return last_error(); }
 
 int ta_record_bytes(const ta_problem* p, int64_t* bytes) {
   Plan P;

@@ -366,6 +366,19 @@ __device__ __forceinline__ bool xcd_bh_block(int i, int nbh, int nl, int& bh, in
 inline unsigned xcd_grid(int64_t nbh, int nl) {
   return (unsigned)(((nbh + kXcds - 1) / kXcds) * kXcds * nl);
 }
+// A launch over a group of nbh (batch, head)s: with at least one per XCD the
+// mapping above; with fewer, each (batch, head)'s blocks are spread over all
+// XCDs in order (linear id = bh * nl + beta), so no XCD idles.  Launch
+// group_grid(nbh, nl) workgroups.
+__device__ __forceinline__ bool group_bh_block(int i, int nbh, int nl, int& bh, int& beta) {
+  if (nbh >= kXcds) return xcd_bh_block(i, nbh, nl, bh, beta);
+  bh = i / nl;
+  beta = i - bh * nl;
+  return bh < nbh;
+}
+inline unsigned group_grid(int64_t nbh, int nl) {
+  return nbh >= kXcds ? xcd_grid(nbh, nl) : (unsigned)(nbh * nl);
+}
 
 // ------------------------------------------------------ vector-ALU dots ---
 
@@ -511,7 +524,7 @@ struct RecordLayout {
 };
 
 struct FwdWorkspaceLayout {
-  int64_t partial;  // E (B, L, H, S, D): w * o per distinct leaf block
+  int64_t partial;  // E (BH, L, S, D): w * o per distinct leaf block
   int64_t total;
 };
 

@@ -22,6 +22,12 @@ struct Plan {
   BwdWorkspaceLayout bws;
 };
 
+// capi.cpp: plan builder and the calling thread's error message
+int make_plan(const ta_problem* p, Plan* P);  // TA_OK or an error code (message set)
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int ok();  // clears the message, returns TA_OK
+const char* last_error();
+
 // pool.hip
 hipError_t launch_pool(const Plan& P, const void* k, char* rec, hipStream_t st);
 hipError_t launch_fill_uniforms(uint64_t seed, int64_t n, float* out, hipStream_t st);
@@ -46,6 +52,10 @@ hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st);
 // leaf_fwd.hip
 hipError_t launch_leaf_fwd(const Plan& P, const void* q, const void* k, const void* v,
                            void* out, char* rec, char* ws, hipStream_t st);
+// The leaf forward of the (batch, head)s bh0 .. bh0 + nbh - 1 only, with their
+// partial rows in `partial` ((nbh, L, S, D) elements of the input type).
+hipError_t launch_leaf_fwd_group(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
+                                 void* partial, int bh0, int nbh, hipStream_t st);
 // leaf_bwd.hip
 hipError_t launch_leaf_bwd(const Plan& P, const void* q, const void* k, const void* v,
                            const void* g, const char* rec, void* dv, char* ws, hipStream_t st);

@@ -10,12 +10,15 @@
 // straight from the S^T accumulator registers.  Each pair's w * o lands in
 // its own slot of the partial buffer; combine_kernel sums the slots of each
 // query in slot order, so the forward is deterministic without atomics.
+// A launch covers the (batch, head)s bh0 .. bh0 + nbh - 1; the partial buffer
+// holds the rows of those only, (nbh, L, S, D), so a caller with a bounded
+// buffer runs the heads in groups (same kernels, same results).
 #include "launch.h"
 
 namespace ta {
 
 struct LeafFwdArgs {
-  int B, L, H, S, NL, LB, causal, coff, npiece;
+  int B, L, H, S, NL, LB, causal, coff, npiece, bh0, nbh;
   float scale_log2;
   const void *q, *k, *v;
   int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh;
@@ -46,7 +49,9 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
   E* Vt = Ks + LBP * KS;    // [D][VS]
 
   int bh, beta;
-  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
+  if (!group_bh_block(blockIdx.x, a.nbh, a.NL, bh, beta)) return;
+  const int64_t prow0 = (int64_t)bh * a.L;  // partial rows of this (batch, head): (prow0 + l) * S + u
+  bh += a.bh0;
   const int bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
   const int start = bs[beta], end = bs[beta + 1];
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(256) void leaf_fwd_kernel(LeafFwdArgs a) {
 
     const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
     const float f = (valid && sum > 0.f) ? a.slot_weight[qh * S + u] / sum : 0.f;
-    E* dst = (E*)a.partial + (qh * S + u) * D;
+    E* dst = (E*)a.partial + ((prow0 + l) * S + u) * D;
 #pragma unroll
     for (int md = 0; md < D / 16; ++md) {
       f32x4 o = zero4();
@@ -165,7 +170,9 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
   E* Ks = Vs + LBP * VS;                    // [LBP][VS]
 
   int bh, piece;
-  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.npiece, bh, piece)) return;
+  if (!group_bh_block(blockIdx.x, a.nbh, a.npiece, bh, piece)) return;
+  const int64_t prow0 = (int64_t)bh * a.L;  // partial rows of this (batch, head): (prow0 + l) * S + u
+  bh += a.bh0;
   const int beta = a.piece_block[(int64_t)bh * a.npiece + piece];
   if (beta < 0) return;
   const int bb = bh / a.H, h = bh - bb * a.H;
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
     F pf[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) pf[kk] = acc_operand<E>(sacc, kk);
-    E* dst = (E*)a.partial + (qh * S + u) * D + 8 * g;
+    E* dst = (E*)a.partial + ((prow0 + l) * S + u) * D + 8 * g;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       f32x4 o0 = zero4(), o1 = zero4();
@@ -305,19 +312,21 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
   }
 }
 
-// out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows.
+// out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows,
+// for the nrows = nbh * L queries of the launch's (batch, head) group.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
-                                                      E* __restrict__ out, int L, int H, int S, int64_t nqh,
+                                                      E* __restrict__ out, int L, int H, int S, int bh0, int64_t nrows,
                                                       int64_t osb, int64_t osl, int64_t osh) {
   constexpr int TPQ = D / 8;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t qh = gid / TPQ;
-  if (qh >= nqh) return;
-  const int part = (int)(gid - qh * TPQ);
+  const int64_t row = gid / TPQ;
+  if (row >= nrows) return;
+  const int part = (int)(gid - row * TPQ);
+  const int64_t bh = bh0 + row / L, l = row % L, bb = bh / H, h = bh - bb * H;
+  const int64_t qh = (bb * L + l) * H + h;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  sum_rows8(acc, partial + qh * S * D + 8 * part, D, slot_count[qh]);
-  const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
+  sum_rows8(acc, partial + row * S * D + 8 * part, D, slot_count[qh]);
   E* o = out + bb * osb + l * osl + h * osh + 8 * part;
   if constexpr (sizeof(E) == 2) {
     typedef __attribute__((ext_vector_type(8))) E e8;
@@ -352,7 +361,7 @@ int leaf_fwd_smem(const Plan& P) {
 
 template <typename E, int D, int LBP>
 static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
-                                char* ws, hipStream_t st) {
+                                void* partial, int bh0, int nbh, hipStream_t st) {
   LeafFwdArgs a;
   a.B = (int)P.B;
   a.L = (int)P.L;
@@ -375,56 +384,63 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   a.piece_start = (const int*)(rec + P.rec.piece_start);
   a.piece_block = (const int*)(rec + P.rec.piece_block);
   a.slot_weight = (const float*)(rec + P.rec.slot_weight);
-  a.partial = ws + P.fws.partial;
+  a.partial = partial;
+  a.bh0 = bh0;
+  a.nbh = nbh;
   if constexpr (sizeof(E) == 2) {
     const int smem = fwd16_smem(D, LBP);
     hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd16_kernel<E, D, LBP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((leaf_fwd16_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.npiece)), dim3(256), smem, st, a);
+    hipLaunchKernelGGL((leaf_fwd16_kernel<E, D, LBP>), dim3(group_grid(nbh, P.npiece)), dim3(256), smem, st, a);
   } else {
     const int smem = fwd_smem_t<E, D, LBP>();
     hipError_t e = hipFuncSetAttribute((const void*)leaf_fwd_kernel<E, D, LBP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(xcd_grid(P.BH, P.geo.NL)), dim3(256), smem, st, a);
+    hipLaunchKernelGGL((leaf_fwd_kernel<E, D, LBP>), dim3(group_grid(nbh, P.geo.NL)), dim3(256), smem, st, a);
   }
-  const int64_t nqh = P.B * P.L * P.H;
-  const int64_t nthr = nqh * (D / 8);
+  const int64_t nrows = (int64_t)nbh * P.L;
+  const int64_t nthr = nrows * (D / 8);
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
                      (const E*)a.partial, (const int*)(rec + P.rec.slot_count), (E*)out, (int)P.L, (int)P.H,
-                     (int)P.S, nqh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2]);
+                     (int)P.S, bh0, nrows, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2]);
   return hipGetLastError();
 }
 
 template <typename E, int D>
 static hipError_t leaf_fwd_lb(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
-                              char* ws, hipStream_t st) {
+                              void* partial, int bh0, int nbh, hipStream_t st) {
   switch (padded_keys(P.geo.LB)) {
-    case 32: return leaf_fwd_impl<E, D, 32>(P, q, k, v, out, rec, ws, st);
-    case 64: return leaf_fwd_impl<E, D, 64>(P, q, k, v, out, rec, ws, st);
-    default: return leaf_fwd_impl<E, D, 128>(P, q, k, v, out, rec, ws, st);
+    case 32: return leaf_fwd_impl<E, D, 32>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    case 64: return leaf_fwd_impl<E, D, 64>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    default: return leaf_fwd_impl<E, D, 128>(P, q, k, v, out, rec, partial, bh0, nbh, st);
   }
 }
 
 template <typename E>
 static hipError_t leaf_fwd_d(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
-                             char* ws, hipStream_t st) {
+                             void* partial, int bh0, int nbh, hipStream_t st) {
   switch (P.D) {
-    case 32: return leaf_fwd_lb<E, 32>(P, q, k, v, out, rec, ws, st);
-    case 64: return leaf_fwd_lb<E, 64>(P, q, k, v, out, rec, ws, st);
-    case 96: return leaf_fwd_lb<E, 96>(P, q, k, v, out, rec, ws, st);
-    default: return leaf_fwd_lb<E, 128>(P, q, k, v, out, rec, ws, st);
+    case 32: return leaf_fwd_lb<E, 32>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    case 64: return leaf_fwd_lb<E, 64>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    case 96: return leaf_fwd_lb<E, 96>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    default: return leaf_fwd_lb<E, 128>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+  }
+}
+
+hipError_t launch_leaf_fwd_group(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
+                                 void* partial, int bh0, int nbh, hipStream_t st) {
+  switch (P.p.dtype) {
+    case TA_F32: return leaf_fwd_d<float>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    case TA_BF16: return leaf_fwd_d<bf16>(P, q, k, v, out, rec, partial, bh0, nbh, st);
+    default: return leaf_fwd_d<f16>(P, q, k, v, out, rec, partial, bh0, nbh, st);
   }
 }
 
 hipError_t launch_leaf_fwd(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec, char* ws,
                            hipStream_t st) {
-  switch (P.p.dtype) {
-    case TA_F32: return leaf_fwd_d<float>(P, q, k, v, out, rec, ws, st);
-    case TA_BF16: return leaf_fwd_d<bf16>(P, q, k, v, out, rec, ws, st);
-    default: return leaf_fwd_d<f16>(P, q, k, v, out, rec, ws, st);
-  }
+  return launch_leaf_fwd_group(P, q, k, v, out, rec, ws + P.fws.partial, 0, (int)P.BH, st);
 }
 
 }  // namespace ta
