@@ -147,6 +147,23 @@ int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v,
                const float* uniforms, uint64_t seed, void* out, float* weights,
                void* record, void* workspace, void* stream);
 
+/* ta_forward without the workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The pair rows the
+ * combine sums (ta_forward's workspace) live in a static device array of
+ * TA_STATIC_SCRATCH_BYTES per GPU (allocated when the library is first used on
+ * that device and held until the process ends); the leaf forward runs over
+ * groups of (batch, head)s whose rows fit in it.  Outputs and record are
+ * bit-identical to ta_forward's.  Problems whose one (batch, head) needs more
+ * (L * num_samples * head_dim * element size bytes) get TA_ERR_UNSUPPORTED.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialized by the
+ * caller.  The stream must belong to the current device.  Allocates nothing. */
+#define TA_STATIC_SCRATCH_BYTES ((int64_t)128 << 20)
+int ta_forward_static(const ta_problem* p, const void* q, const void* k, const void* v,
+                      const float* uniforms, uint64_t seed, void* out, float* weights, void* record,
+                      void* stream);
+
 /* Streaming forward of the deterministic mode for bfloat16 / float16 inputs:
  * out = W V with _deterministic_attention's weights (_tree_mha.py:286-318)
  * without materializing the (L, N) weights (memory O(L D)).  q and out

@@ -79,6 +79,7 @@ EXPORTS = (
     "ta_unpack_paths",
     "ta_replay",
     "ta_forward_replay",
+    "ta_forward_static",
 )
 
 _lock = threading.Lock()
@@ -144,6 +145,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_replay.argtypes = [P, vp, vp, vp, vp, vp]
     lib.ta_forward_replay.restype = ctypes.c_int
     lib.ta_forward_replay.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ta_forward_static.restype = ctypes.c_int
+    lib.ta_forward_static.argtypes = [P, vp, vp, vp, vp, ctypes.c_uint64, vp, vp, vp, vp]
 
 
 def load() -> ctypes.CDLL:
