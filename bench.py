@@ -35,6 +35,10 @@ CONFIGS = {
     "C4": (1, 131072, 8, 128, "bfloat16", 2, 128, 16, False, "scaled"),
     "C5-D32": (8, 8192, 32, 32, "float16", 2, 32, 8, True, "skewed"),
     "C5-D96": (8, 8192, 32, 96, "float16", 2, 32, 8, True, "skewed"),
+    # the reference's own tree (binary, one token per leaf, Haar keys: the op-level
+    # hierarchical_attention and the adapter's default stochastic tree) at C3's shape
+    "REF-16k": (2, 16384, 16, 128, "bfloat16", 2, 1, 16, False, "normal"),
+    "REF-64k": (2, 65536, 16, 128, "bfloat16", 2, 1, 16, False, "normal"),
 }
 
 
@@ -62,6 +66,10 @@ def parse():
     ap.add_argument("--phases-only", action="store_true", help="only run the per-phase loop (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM counters)")
+    ap.add_argument("--dense-cols", type=int, default=0,
+                    help="widest tree level run as dense level tiles (0: the library's defaults)")
+    ap.add_argument("--causal", choices=("config", "on", "off"), default="config",
+                    help="override the config's causality")
     ap.add_argument("--mode", default="stochastic", choices=("stochastic", "deterministic"),
                     help="deterministic: the exact mode of the reference tree (adapter path, Haar keys) at the "
                          "config's B, L, H, D, dtype and causality (default config C2)")
@@ -103,7 +111,8 @@ def read_traffic(phase: str, config: str):
 
 # Queries timed per config by the CPU baseline (all heads of batch element 0, the
 # last CPU_QUERIES[c] positions, against the full-length tree, keys and values).
-CPU_QUERIES = {"C1": 1024, "C2": 1024, "C3": 512, "C4": 128, "C5-D32": 1024, "C5-D96": 512}
+CPU_QUERIES = {"C1": 1024, "C2": 1024, "C3": 512, "C4": 128, "C5-D32": 1024, "C5-D96": 512, "REF-16k": 512,
+               "REF-64k": 256}
 
 
 def cpu_model() -> str:
@@ -266,6 +275,8 @@ def main() -> int:
     from treeattention_amd.function import TreeOptions, _prep, _strides, make_problem
 
     cfg = CONFIGS[args.config]
+    if args.causal != "config":
+        cfg = cfg[:8] + (args.causal == "on",) + cfg[9:]
     B, L, H, D, dts, b, LB, S, causal, kind = cfg
     dtype = getattr(torch, dts)
     dev = torch.device("cuda:0")
@@ -281,7 +292,7 @@ def main() -> int:
     q.requires_grad_(True)
     k.requires_grad_(True)
     v.requires_grad_(True)
-    kw = dict(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, seed=0)
+    kw = dict(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, seed=0, dense_cols=args.dense_cols)
 
     def step():
         q.grad = k.grad = v.grad = None

@@ -69,7 +69,9 @@ typedef struct ta_problem {
   int32_t tree_mode;     /* TA_TREE_* */
   int32_t causal;        /* TA_CAUSAL_* */
   int32_t dtype;         /* TA_F32 / TA_BF16 / TA_F16 */
-  int32_t reserved;
+  int32_t dense_cols;    /* tree levels with at most this many children run as dense level
+                            tiles, wider ones per sampled path (0: the library's defaults);
+                            changes no result beyond rounding, for tuning and tests */
   float scale;           /* leaf-block softmax scale */
   float max_logit;       /* child logits are clamped to +-max_logit/2 (binary compat trees:
                             the left/right logit to +-max_logit, _autograd.py:202) */

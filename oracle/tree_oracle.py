@@ -434,7 +434,8 @@ def tree_sample(
     for bb in range(B):
         for h in range(H):
             Q = q[bb, :, h].astype(np.float64)  # (L,D)
-            X = np.clip(Q @ C[bb, h].T, -half, half)  # (L,NS)
+            Cb = C[bb, h]
+            X = lambda cols: np.clip(path_logits(Q, Cb, cols), -half, half)  # noqa: E731
             node = np.zeros((L, S), dtype=np.int64)
             acc = np.zeros((L, S))
             if causal and T > 0:
@@ -442,12 +443,12 @@ def tree_sample(
                 digits = np.stack([(blk_t // b ** (T - 1 - d)) % b for d in range(T)], axis=-1)
                 bnode = np.stack([blk_t // b ** (T - d) for d in range(T)], axis=-1)  # (L,T)
                 cols_b = np.asarray(off[1:T + 1])[None, :, None] + b * bnode[:, :, None] + jj  # (L,T,b)
-                xb = np.take_along_axis(X, cols_b.reshape(L, -1), axis=1).reshape(L, T, b)
+                xb = X(cols_b)
                 logp_b = xb - _lse(xb)[..., None]
                 logA = causal_boundary_logmass(logp_b, digits)  # (L,T+1)
             for d in range(T):
                 cols = off[d + 1] + b * node[..., None] + jj  # (L,S,b)
-                x = np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+                x = X(cols)
                 logp = x - _lse(x)[..., None]
                 if causal:
                     on_b = node == bnode[:, d][:, None]  # (L,S)
@@ -467,6 +468,17 @@ def tree_sample(
     return idx, lp, margins
 
 
+def path_logits(Q, C, cols):
+    """``x[l, s, j] = Q[l] . C[cols[l, s, j]]`` for one (batch, head): ``Q`` (L, D),
+    ``C`` (NS, D), ``cols`` (L, S, b).  From the dense ``Q C^T`` when it is small,
+    else by gathering only the rows the paths visit (linear in L)."""
+    L = Q.shape[0]
+    if L * C.shape[0] <= 1 << 25:
+        X = Q @ C.T
+        return np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(cols.shape)
+    return np.matmul(C[cols.reshape(L, -1)], Q[:, :, None])[..., 0].reshape(cols.shape)
+
+
 def path_logprobs(q, C, branching, num_leaf_blocks, idx, max_logit=1e3):
     """Uncorrected ``log P(leaf)`` of given sampled leaf blocks (B,L,H,S).
 
@@ -484,13 +496,13 @@ def path_logprobs(q, C, branching, num_leaf_blocks, idx, max_logit=1e3):
     lp = np.zeros((B, L, H, S))
     for bb in range(B):
         for h in range(H):
-            X = np.clip(q[bb, :, h].astype(np.float64) @ C[bb, h].T, -half, half)
+            Q = q[bb, :, h].astype(np.float64)
             leaf = idx[bb, :, h]
             for d in range(T):
                 node = leaf // b ** (T - d)
                 js = (leaf // b ** (T - 1 - d)) % b
-                cols = off[d + 1] + b * node[..., None] + jj
-                x = np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+                cols = off[d + 1] + b * node[..., None] + jj  # (L, S, b)
+                x = np.clip(path_logits(Q, C[bb, h], cols), -half, half)
                 logp = x - _lse(x)[..., None]
                 lp[bb, :, h] += np.take_along_axis(logp, js[..., None], axis=-1)[..., 0]
     return lp
@@ -628,13 +640,14 @@ def tree_backward(q, k, v, C, branching, leaf_block, idx, w, dout, causal, scale
 
 def head_fwd_bwd(q, k, v, dout, C, branching, leaf_block, idx, causal, scale, max_logit=1e3):
     """``tree_forward`` + ``tree_backward`` of ONE (batch, head) on given paths,
-    organized by leaf block so that full-size heads run in seconds.
+    organized by leaf block so that full-size heads run in seconds (child
+    logits only along the sampled paths: linear in L for any tree).
 
     Same mathematics as ``leaf_attention`` / ``sample_weights(path_logprobs)``
     / ``tree_backward`` (``_tree_mha.py:396-407``, ``_autograd.py:744-858``),
     but every (query, sample) pair of a leaf block is processed as one matrix
     product against that block's keys and values, and the child-logit
-    gradient is a dense ``(L, NS)`` matrix ``G`` with ``dq += G C`` and
+    gradient is a sparse ``(L, NS)`` matrix ``G`` with ``dq += G C`` and
     ``dC = G^T q``.  Pinned against those functions in
     ``tests/test_oracle.py::test_head_fwd_bwd_matches_explicit``.
 
@@ -690,24 +703,30 @@ def head_fwd_bwd(q, k, v, dout, C, branching, leaf_block, idx, causal, scale, ma
         dv[beta * LB:(beta + 1) * LB] = (a * ws[:, None]).T @ Gl
     dq = dq_pair.sum(axis=1)
 
+    # child logits only along the sampled paths, so trees with many nodes per
+    # level stay linear in L; G (queries x summary rows) is a sparse matrix
+    from scipy import sparse
+
     half = max_logit / 2
-    Xr = q64 @ C64.T
-    X = np.clip(Xr, -half, half)
-    live = (Xr >= -half) & (Xr <= half)
-    G = np.zeros_like(X)
     jj = np.arange(b)
     rows = np.broadcast_to(np.arange(L)[:, None, None], (L, S, b))
+    gr, gc, gv = [], [], []
     for d in range(T):
         node = idx // b ** (T - d)
         jstar = (idx // b ** (T - 1 - d)) % b
         cols = off[d + 1] + b * node[..., None] + jj  # (L, S, b)
-        x = np.take_along_axis(X, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+        xr = path_logits(q64, C64, cols)
+        x = np.clip(xr, -half, half)
         p = np.exp(x - _lse(x)[..., None])
-        lv = np.take_along_axis(live, cols.reshape(L, -1), axis=1).reshape(L, S, b)
+        lv = (xr >= -half) & (xr <= half)
         dx = dlp[..., None] * ((jj == jstar[..., None]) - p) * lv
-        np.add.at(G, (rows.reshape(-1), cols.reshape(-1)), dx.reshape(-1))
+        gr.append(rows.reshape(-1))
+        gc.append(cols.reshape(-1))
+        gv.append(dx.reshape(-1))
+    G = sparse.coo_matrix((np.concatenate(gv), (np.concatenate(gr), np.concatenate(gc))),
+                          shape=(L, C64.shape[0])).tocsr()  # duplicate entries add
     dq += G @ C64
-    dC = G.T @ q64
+    dC = np.asarray(G.T @ q64)
     return dict(out=out, weights=w, lp=lp, dq=dq, dC=dC, dk_leaf=dk, dv=dv)
 
 

@@ -216,3 +216,91 @@ def test_full_size_complete_head(name):
         e = rel(one(got), ref)
         print(f"  {nm} rel err {e:.3g}", flush=True)
         assert e < 2e-2, (nm, e)
+
+
+# The reference's own tree (binary, one token per leaf, Haar keys) at L=16384:
+# the sampler evaluates its deep levels per sampled path and the backward runs
+# them in node-major bands, so memory and work stay linear in L.
+REF = (2, 16384, 16, 128, torch.bfloat16, 16)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_tree_full_size(causal):
+    """Non-causal: one complete (batch, head) against the oracle (leaves,
+    weights, out, dq, dk, dv); causal (the reference's coupled sampler and
+    hybrid head): the last 64 queries' leaves, out and dq rows against the
+    float64 restatement on the GPU's own paths.  Both: the workspace is linear
+    in L and the whole-problem identities hold."""
+    from oracle import ref_torch as R
+    from treeattention_amd import _lib
+    from treeattention_amd.function import TreeOptions, make_problem, record_views, tree_backward, tree_forward
+
+    B, L, H, D, dtype, S = REF
+    print(f"[case] reference tree full size causal={causal}: B={B} L={L} H={H} D={D} S={S}", flush=True)
+    q, k, v, do = inputs(B, L, H, D, dtype, "normal")
+    opts = TreeOptions(num_samples=S, branching=2, leaf_block=1, tree_mode="compat", causal=causal, seed=0)
+    _, fws, bws = _lib.byte_sizes(make_problem(q, k, v, opts))
+    per_qh = (fws + bws) / (B * L * H)
+    print(f"  workspaces {fws / 2**30:.2f} + {bws / 2**30:.2f} GiB ({per_qh / 1024:.1f} KiB per query-head)", flush=True)
+    assert per_qh < 16 * 1024  # linear in L: a few KiB per query-head (the dense G^T would be 64 KiB)
+    out, w, rec = tree_forward(q, k, v, opts)
+    leaves_t, _ = record_views(q, k, v, opts, rec)
+    dq, dk, dv = tree_backward(q, k, v, w, rec, do, opts)
+    torch.cuda.synchronize()
+    for t in (out, dq, dk, dv):
+        assert torch.isfinite(t.float()).all()
+    assert (w >= 0).all() and (w.sum(-1) - 1).abs().max().item() < 1e-5
+    assert rel(dv.float().sum(1).cpu().numpy(), do.float().sum(1).cpu().numpy()) < 2e-2
+    dkf = dk.float()
+    assert (dkf.sum(1).norm(dim=-1) / dkf.pow(2).sum((1, 3)).sqrt()).max().item() < 2e-2
+    T = 14
+    bb, h = B - 1, H - 1
+    one = lambda t: t[bb, :, h].float().cpu().numpy().astype(np.float64)  # noqa: E731  (L, D)
+    qh, kh, vh, doh = one(q), one(k), one(v), one(do)
+    lv = leaves_t[bb, :, h].cpu().numpy().astype(np.int64)  # (L, S)
+    if not causal:
+        C = O.summaries(kh[None, :, None], 2, 1, "compat")
+        s_, t_, j_ = np.meshgrid(np.arange(S), np.arange(T), np.arange(2), indexing="ij")
+        flat = ((((bb * L + np.arange(L)[:, None, None, None]) * H + h) * S + s_[None]) * T + t_[None]) * 2 + j_[None]
+        U = uniforms_at(0, flat.reshape(-1)).reshape(1, L, 1, S, T, 2)
+        idx_o, _, margins = O.tree_sample(qh[None, :, None], C, 2, 1, U, False, N=L)
+        clean = margins.min(axis=-1)[0, :, 0] > 1e-3
+        assert not ((lv != idx_o[0, :, 0]) & clean).any()
+        assert clean.mean() > 0.9
+        r = O.head_fwd_bwd(qh, kh, vh, doh, C[0, 0], 2, 1, lv, False, 1.0 / math.sqrt(D))
+        dk_ref = r["dk_leaf"] + O.pool_adjoint(r["dC"][None, None], L, 2, 1, "compat")[0, :, 0]
+        assert rel(w[bb, :, h].cpu().numpy(), r["weights"]) < 1e-4
+        for nm, got, ref in (("out", out, r["out"]), ("dq", dq, r["dq"]), ("dk", dk, dk_ref), ("dv", dv, r["dv"])):
+            e = rel(one(got), ref)
+            print(f"  {nm} rel err {e:.3g}", flush=True)
+            assert e < 2e-2, (nm, e)
+        return
+    # causal: the last SUB query positions, every (batch, head) of them -- the
+    # reference's sampler couples all (batch, head, sample) lanes of a position
+    t0 = L - SUB
+    allq = lambda t: t.float().cpu().numpy().astype(np.float64).transpose(1, 0, 2, 3)  # noqa: E731  (L, B, H, D)
+    qa, ka, va, da_ = allq(q), allq(k), allq(v), allq(do)
+    kn = torch.tensor(O.haar_inorder(ka))  # (L-1, B, H, D) heap-ordered node keys
+    bb_, ll_, hh_, s_, t_, j_ = np.meshgrid(np.arange(B), np.arange(t0, L), np.arange(H), np.arange(S), np.arange(T),
+                                            np.arange(2), indexing="ij")
+    flat = (((((bb_ * L + ll_) * H + hh_) * S + s_) * T + t_) * 2 + j_).reshape(-1)
+    U = np.full((B, L, H, S, T, 2), 0.5, dtype=np.float32)
+    U[:, t0:] = uniforms_at(0, flat).reshape(B, SUB, H, S, T, 2)
+    qs = torch.tensor(qa[t0:], requires_grad=True)
+    idx_o, _, margins, _ = R.sample_causal(qs.detach(), kn, L, U, offset=t0)
+    clean = margins.numpy().min(axis=-1) > 1e-3
+    lvs = leaves_t[:, t0:].cpu().numpy().astype(np.int64).transpose(1, 0, 2, 3)  # (SUB, B, H, S)
+    assert not ((lvs != idx_o.numpy()) & clean).any(), f"{int(((lvs != idx_o.numpy()) & clean).sum())} clean differ"
+    assert clean.mean() > 0.9
+    idx, lp, _, _ = R.sample_causal(qs, kn, L, U, offset=t0, forced=torch.tensor(lvs))
+    wr = torch.softmax(lp, dim=-1)  # (SUB, B, H, S)
+    vb = torch.tensor(va).permute(1, 2, 0, 3)  # (B, H, L, D)
+    gi = idx.clamp(0, L - 1).permute(1, 2, 0, 3).reshape(B, H, -1, 1).expand(-1, -1, -1, D)
+    vg = torch.gather(vb, 2, gi).reshape(B, H, SUB, S, D).permute(2, 0, 1, 3, 4)
+    o_ref = (wr[..., None] * vg).sum(-2)  # (SUB, B, H, D)
+    o_ref.backward(torch.tensor(da_[t0:]))
+    assert rel(w[:, t0:].cpu().numpy().transpose(1, 0, 2, 3), wr.detach().numpy()) < 1e-4
+    for nm, got, ref in (("out", allq(out)[t0:], o_ref.detach().numpy()), ("dq", allq(dq)[t0:], qs.grad.numpy())):
+        e = rel(got, ref)
+        print(f"  {nm} rel err {e:.3g} (last {SUB} positions, all heads)", flush=True)
+        assert e < 2e-2, (nm, e)

@@ -52,19 +52,21 @@ def f64(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", backward=True, scale=None, N=None):
+def run_case(B, L, H, D, S, b, LB, mode, causal, dtype, seed=0, kind="normal", backward=True, scale=None, N=None,
+             dense_cols=0):
     from treeattention_amd.function import TreeOptions, record_views, tree_backward, tree_forward
 
     N = L if N is None else N
-    print(f"[case] B={B} L={L} N={N} H={H} D={D} S={S} b={b} LB={LB} mode={mode} causal={causal} {dtype} {kind}",
-          flush=True)
+    print(f"[case] B={B} L={L} N={N} H={H} D={D} S={S} b={b} LB={LB} mode={mode} causal={causal} {dtype} {kind} "
+          f"dense_cols={dense_cols}", flush=True)
     q, k, v, do = make_inputs(B, L, H, D, dtype, seed, kind, N=N)
     nl = N // LB
     T = O.tree_depth(nl, b)
     U = O.uniforms(seed, (B, L, H, S, T, b))
     dev = torch.device("cuda:0")
     qg, kg, vg, dog = (x.to(dev) for x in (q, k, v, do))
-    opts = TreeOptions(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, causal=causal, scale=scale, seed=seed)
+    opts = TreeOptions(num_samples=S, branching=b, leaf_block=LB, tree_mode=mode, causal=causal, scale=scale, seed=seed,
+                       dense_cols=dense_cols)
     out, w, rec = tree_forward(qg, kg, vg, opts, torch.from_numpy(U).to(dev))
     leaves_t, sums_t = record_views(qg, kg, vg, opts, rec)
     torch.cuda.synchronize()
@@ -156,6 +158,31 @@ def test_c5_like_skewed_fp16_causal(D):
 
 def test_fp32_causal_natural_b4():
     run_case(1, 256, 2, 64, 8, 4, 16, "natural", True, torch.float32)
+
+
+# Deep levels evaluated per sampled path (sampler) and in node-major bands
+# (backward): dense_cols caps the levels that run as dense tiles, so small
+# problems take the paths that wide trees (the reference tree at long L) take.
+@pytest.mark.parametrize("dtype,S", [(torch.float32, 8), (torch.bfloat16, 16)])
+def test_sparse_levels_reference_tree(dtype, S):
+    run_case(2, 256, 2, 64, S, 2, 1, "compat", False, dtype, dense_cols=8)  # levels 3..7 sparse, one 5-depth band
+
+
+def test_sparse_levels_two_bands_lb16():
+    run_case(1, 2048, 2, 64, 8, 2, 16, "compat", False, torch.bfloat16, dense_cols=4)  # leaf dq rows + 2 bands
+
+
+def test_sparse_levels_b4_causal():
+    run_case(1, 1024, 2, 128, 16, 4, 4, "natural", True, torch.bfloat16, dense_cols=16)
+
+
+@pytest.mark.parametrize("D", [32, 96])
+def test_sparse_levels_natural_b2_skewed_fp16(D):
+    run_case(2, 512, 2, D, 8, 2, 2, "natural", True, torch.float16, kind="skewed", dense_cols=16)
+
+
+def test_sparse_levels_fp32_natural_b2_causal_N_gt_L():
+    run_case(1, 200, 2, 64, 8, 2, 1, "natural", True, torch.float32, N=256, dense_cols=4)
 
 
 @pytest.mark.parametrize("b,L,LB,causal", [(2, 8192, 16, False), (4, 4096, 4, True)])

@@ -41,14 +41,14 @@ def f64(t):
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def gpu_run(q, k, v, dout, U, S, causal, dtype):
+def gpu_run(q, k, v, dout, U, S, causal, dtype, dense_cols=0):
     """Node-key tree on the GPU: (out (L,B,H,D), weights (L,B,H,S), leaves (L,B,H,S), dq, dk, dv)."""
     from treeattention_amd.function import TreeOptions, record_views, tree_backward, tree_forward
 
     dev = torch.device("cuda:0")
     qg, kg, vg, dg = (torch.as_tensor(x).to(dtype).to(dev) for x in (q, k, v, dout))
     opts = TreeOptions(num_samples=S, branching=2, leaf_block=1, tree_mode="nodekeys", causal=causal, seed=0,
-                       layout="lbhd")
+                       layout="lbhd", dense_cols=dense_cols)
     out, w, rec = tree_forward(qg, kg, vg, opts, torch.as_tensor(U).to(dev))
     leaves = record_views(qg, kg, vg, opts, rec)[0]  # (B, L, H, S) in the problem's (batch, position) order
     dq, dk, dv = tree_backward(qg, kg, vg, w, rec, dg, opts)
@@ -113,13 +113,16 @@ def _oracle_run(q, k, v, dout, U, S, causal, forced=None):
             vt.grad.numpy())
 
 
-@pytest.mark.parametrize("L,B,H,D,S,dtype", [
-    (256, 2, 2, 32, 8, torch.float32),
-    (256, 1, 4, 64, 16, torch.bfloat16),
-    (64, 1, 2, 32, 64, torch.float32),  # L <= S: every query sampled, no exact head
+@pytest.mark.parametrize("L,B,H,D,S,dtype,dense_cols", [
+    (256, 2, 2, 32, 8, torch.float32, 0),
+    (256, 1, 4, 64, 16, torch.bfloat16, 0),
+    (64, 1, 2, 32, 64, torch.float32, 0),  # L <= S: every query sampled, no exact head
+    # deep levels per sampled path and in bands (boundary-mass gradient at band depths)
+    (256, 2, 2, 32, 8, torch.float32, 4),
+    (512, 1, 2, 64, 16, torch.bfloat16, 8),
 ])
-def test_gpu_reference_causal_against_restatement(L, B, H, D, S, dtype):
-    print(f"[case] reference causal L={L} B={B} H={H} D={D} S={S} {dtype}", flush=True)
+def test_gpu_reference_causal_against_restatement(L, B, H, D, S, dtype, dense_cols):
+    print(f"[case] reference causal L={L} B={B} H={H} D={D} S={S} {dtype} dense_cols={dense_cols}", flush=True)
     g = torch.Generator().manual_seed(L + S)
     q = torch.randn(L, B, H, D, generator=g).to(dtype).double().numpy()
     k = (0.5 * torch.randn(L - 1, B, H, D, generator=g)).to(dtype).double().numpy()
@@ -127,7 +130,7 @@ def test_gpu_reference_causal_against_restatement(L, B, H, D, S, dtype):
     do = torch.randn(L, B, H, D, generator=g).to(dtype).double().numpy()
     T = (L - 1).bit_length()
     U = O.uniforms(11, (B, L, H, S, T, 2))
-    out, w, leaves, dq, dk, dv = gpu_run(q, k, v, do, U, S, True, dtype)
+    out, w, leaves, dq, dk, dv = gpu_run(q, k, v, do, U, S, True, dtype, dense_cols)
     out_o, w_o, info, dq_o, dk_o, dv_o = _oracle_run(q, k, v, do, U, S, True)
     t0 = S if L > S else 0
     clean = info["margins"].numpy().min(axis=-1) > 1e-3

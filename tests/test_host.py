@@ -153,3 +153,37 @@ def test_cpu_tensors_are_rejected_not_computed():
     x = torch.zeros(1, 64, 1, 32)
     with pytest.raises(ValueError):
         ta.tree_attention(x, x, x, num_samples=4)
+
+
+def _ref_tree_problem(L, causal=False):
+    from treeattention_amd import _lib
+
+    p = _lib.Problem()
+    p.B, p.L, p.H, p.D, p.N = 2, L, 16, 128, L
+    p.num_samples, p.branching, p.leaf_block = 16, 2, 1
+    p.tree_mode = _lib.TA_TREE_NODEKEYS
+    p.causal = _lib.TA_CAUSAL_REFERENCE if causal else _lib.TA_CAUSAL_NONE
+    p.dtype, p.scale, p.max_logit = _lib.TA_BF16, 0.1, 1e3
+    for f in ("q_strides", "k_strides", "v_strides", "o_strides", "g_strides"):
+        getattr(p, f)[:] = (16 * 128, 2 * 16 * 128, 128)  # (L, B, H, D) op-level layout
+    p.w_strides[:] = (16 * 16, 2 * 16 * 16, 16)
+    return p
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_tree_buffers_linear_in_length(causal):
+    """On the reference's tree (binary, one token per leaf) the sampler's deep
+    levels run per sampled path and the backward's in bands, so the forward and
+    backward workspaces grow linearly with L (the op-level problem at B=2, H=16,
+    D=128, S=16); the record's bucket table grows as L^2 / 256."""
+    from treeattention_amd import _lib
+
+    sizes = {L: _lib.byte_sizes(_ref_tree_problem(L, causal)) for L in (4096, 16384, 65536)}
+    for L in sizes:
+        rec, fws, bws = sizes[L]
+        print(L, rec / 2**30, fws / 2**30, bws / 2**30)
+        assert fws == 0  # the leaf stage of one-token leaves is a value gather
+    r16, r64 = sizes[16384][2], sizes[65536][2]
+    assert r64 < 4.4 * r16  # linear (a dense child-logit gradient would be 16x)
+    assert sizes[65536][2] < 24 * 2**30  # fits one GPU with room (was 565 GB)
+    assert sizes[65536][0] < 16 * 2**30

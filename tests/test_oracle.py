@@ -449,3 +449,16 @@ def test_uniforms_at_matches_full_tensor():
     u = O.uniforms(9, (3, 7, 5))
     flat = np.array([0, 1, 2, 3, 4, 17, 50, 101, 104])
     np.testing.assert_array_equal(O.uniforms_at(9, flat), u.reshape(-1)[flat])
+
+
+def test_path_logits_gathered_equals_dense():
+    """``path_logits``' gathered form (large trees) against the dense product."""
+    rng = np.random.default_rng(31)
+    Q = rng.standard_normal((300, 16))
+    C = rng.standard_normal((200000, 16))
+    cols = rng.integers(0, C.shape[0], size=(300, 5, 2))
+    got = O.path_logits(Q, C, cols)  # 300 * 200000 > 2^25: the gathered form
+    ref = np.einsum("ld,lsjd->lsj", Q, C[cols])
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    small = O.path_logits(Q, C[:1000], cols % 1000)  # the dense form
+    np.testing.assert_allclose(small, np.einsum("ld,lsjd->lsj", Q, C[cols % 1000]), rtol=1e-12, atol=1e-12)

@@ -39,7 +39,7 @@ class Problem(ctypes.Structure):
         ("tree_mode", ctypes.c_int32),
         ("causal", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("dense_cols", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("max_logit", ctypes.c_float),
         ("q_strides", _I64x3),

@@ -157,6 +157,7 @@ def tree_attention(
     return_weights: bool = False,
     causal_mode: str = "auto",
     paths: torch.Tensor | None = None,
+    dense_cols: int = 0,
 ):
     """Stochastic tree attention on ``(B, L, H, D)`` tensors.
 
@@ -169,11 +170,11 @@ def tree_attention(
     causal included (``causal_mode="auto"`` selects the reference's causal
     semantics on that tree; see ``TreeOptions``).  ``paths`` (non-causal):
     packed path bits ``(L, B, H, S, path_bytes(L // leaf_block))`` uint8 to
-    replay instead of sampling (``pack_paths``).
+    replay instead of sampling (``pack_paths``).  ``dense_cols``: see ``TreeOptions`` (tuning).
     """
     opts = TreeOptions(num_samples=int(num_samples), branching=int(branching), leaf_block=int(leaf_block),
                        tree_mode=tree_mode, causal=bool(causal), causal_mode=causal_mode, scale=softmax_scale,
-                       max_logit=float(max_logit), seed=int(seed), layout="bshd")
+                       max_logit=float(max_logit), seed=int(seed), layout="bshd", dense_cols=int(dense_cols))
     out, weights = TreeAttentionFunction.apply(q, k, v, opts, uniforms, paths)
     return (out, weights) if return_weights else out
 

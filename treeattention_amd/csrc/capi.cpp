@@ -109,6 +109,29 @@ int make_plan(const ta_problem* p, Plan* P) {
   for (int lam = 1; lam <= T; ++lam) G.off[lam + 1] = G.off[lam] + (int)align32(G.pw[lam]);
   G.NS = G.off[T + 1];
   if ((int64_t)G.NS * D * 4 * P->BH > ((int64_t)1 << 40)) return fail(TA_ERR_UNSUPPORTED, "tree too large");
+  // The sampler's level tiles cost O(L * level width); levels with more than
+  // kSampleDenseCols children (b = 2 or 4) are evaluated per sampled item instead.
+  if (p->dense_cols < 0) return fail(TA_ERR_INVALID, "dense_cols must be >= 0 (got %d)", p->dense_cols);
+  const int64_t scols = p->dense_cols > 0 ? p->dense_cols : kSampleDenseCols;
+  P->sample_dense = T;
+  if (b == 2 || b == 4)
+    for (int d = 0; d < T; ++d)
+      if (G.pw[d + 1] > scols) {
+        P->sample_dense = d;
+        break;
+      }
+  // Likewise the backward's dense G tiles (and their G^T rows in the
+  // workspace) cover levels with at most kTreeDenseCols children; deeper ones
+  // run in the band kernels, linear in the sampled pairs.
+  const int64_t tcols = p->dense_cols > 0 ? p->dense_cols : kTreeDenseCols;
+  P->tree_dense = T;
+  if (b == 2 || b == 4)
+    for (int d = 0; d < T; ++d)
+      if (G.pw[d + 1] > tcols) {
+        P->tree_dense = d;
+        break;
+      }
+  const int64_t NSd = G.off[P->tree_dense + 1];  // dense rows
 
   // bucketing: one count per (leaf block, chunk of kQueryChunk queries)
   P->qc = kQueryChunk;
@@ -123,7 +146,7 @@ int make_plan(const ta_problem* p, Plan* P) {
   // 64 so the product has about 512 workgroups (two per CU)
   const int64_t qtiles = (L + kQueryTile - 1) / kQueryTile;
   P->Lp = qtiles * kQueryTile;
-  const int64_t rowchunks = (G.NS / 16 + 23) / 24;
+  const int64_t rowchunks = (NSd / 16 + 23) / 24 > 0 ? (NSd / 16 + 23) / 24 : 1;
   const int64_t kblocks = P->Lp / 64;
   int64_t qsplit = (512 + rowchunks * P->BH - 1) / (rowchunks * P->BH);
   if (qsplit < 1) qsplit = 1;
@@ -139,6 +162,7 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.sum_lo = r.take(half ? P->BH * G.NS * D * es : 0);
   P->rec.sum_t = r.take(P->BH * G.NS * D * es);
   P->rec.means = r.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : P->BH * NL * D * 4);
+  P->rec.segs = r.take(p->tree_mode == TA_TREE_NODEKEYS || NL < 128 ? 0 : P->BH * (NL / 64 + NL / 4096) * D * 4);
   P->rec.leaf = r.take(BLHS * 4);
   P->rec.slot_leaf = r.take(BLHS * 4);
   P->rec.slot_weight = r.take(BLHS * 4);
@@ -151,22 +175,25 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->nseg = (int)((NL * P->nchunk + 16383) / 16384);  // segments of 1024 threads x 16 counts
   P->rec.seg_sum = r.take(P->BH * P->nseg * 4);
   P->rec.dstar = r.take(p->causal == TA_CAUSAL_REFERENCE ? L * 4 : 0);
+  P->rec.logA = r.take(p->causal == TA_CAUSAL_EXACT && P->sample_dense < T ? B * L * H * (T + 1) * 4 : 0);
   P->rec.total = r.at;
+  const bool lb1 = LB == 1;  // leaf stage: a value gather, no pair rows
   Carver f;
-  P->fws.partial = f.take(BLHS * D * es);
+  P->fws.partial = f.take(lb1 ? 0 : BLHS * D * es);
   P->fws.total = f.at;
   Carver w;
   P->bws.delta = w.take(BLHS * 4);
-  P->bws.dq_part = w.take(BLHS * D * es);
+  P->bws.dq_part = w.take(!lb1 || P->tree_dense < T ? BLHS * D * es : 0);
   P->bws.dlogp = w.take(BLHS * 4);
-  P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : B * N * H * D * 4);
-  P->bws.gt = w.take(P->BH * G.NS * P->Lp * es);
+  P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS || lb1 ? 0 : B * N * H * D * 4);
+  P->bws.gt = w.take(P->BH * NSd * P->Lp * es);
   P->bws.qt = w.take(P->BH * D * P->Lp * es);
-  P->bws.dsum_part = w.take(qsplit * P->BH * G.NS * D * 4);
+  P->bws.dsum_part = w.take(qsplit * P->BH * NSd * D * 4);
   P->bws.dsum = w.take(P->BH * G.NS * D * 4);
   const bool rc = p->causal == TA_CAUSAL_REFERENCE;
   P->bws.rc_coef = w.take(rc ? B * L * H * T * 4 : 0);
   P->bws.rc_rho = w.take(rc ? B * L * H * T * 4 : 0);
+  P->bws.rc_g = w.take(rc ? B * L * H * T * 4 : 0);
   P->bws.total = w.at;
 
   if (rc && ref_sample_smem(*P) > 160 * 1024)
@@ -276,7 +303,8 @@ int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const voi
   const int rc = make_plan(p, &P);
   if (rc) return rc;
   const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
-  if (!q || !v || !out || !record || !workspace || (need_k && !k) || !aligned16(q) || !aligned16(v) ||
+  const bool need_ws = P.fws.total > 0;  // leaf_block 1 needs none
+  if (!q || !v || !out || !record || (need_ws && !workspace) || (need_k && !k) || !aligned16(q) || !aligned16(v) ||
       !aligned16(out) || !aligned16(record) || !aligned16(workspace) || (need_k && !aligned16(k)))
     return fail(TA_ERR_INVALID, "q/k/v/out/record/workspace must be 16-byte aligned device pointers");
   return launch_status(launch_leaf_fwd(P, q, k, v, out, (char*)record, (char*)workspace, (hipStream_t)stream),

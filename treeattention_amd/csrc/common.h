@@ -20,6 +20,8 @@ constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 cov
 constexpr int kMaxSamples = 64;   // one wavefront lane per sample
 constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
 constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
+constexpr int kSampleDenseCols = 1024;  // widest level the sampler evaluates as level tiles
+constexpr int kTreeDenseCols = 1024;    // widest level the backward's dense G tiles cover
 constexpr int kDetMaxLeaves = TA_DET_MAX_LEAVES;  // deterministic mode: leaves per row held in LDS
 
 // Tree geometry.  Child summaries are stored level-major: level lam (1..T)
@@ -509,6 +511,7 @@ struct RecordLayout {
   int64_t sum_lo;      // E (BH, NS, D): summaries - hi
   int64_t sum_t;       // E (BH, D, NS): hi, transposed (float inputs: float)
   int64_t means;       // float (BH, NL, D) leaf-block means
+  int64_t segs;        // float: sums of 64 and of 64^2 consecutive means (NL >= 128)
   int64_t leaf;        // int (B, L, H, S): leaf block of each sample
   int64_t slot_leaf;   // int (B, L, H, S): distinct leaf blocks, ascending
   int64_t slot_weight; // float (B, L, H, S): summed weight per distinct leaf block
@@ -520,6 +523,7 @@ struct RecordLayout {
   int64_t piece_block; // int (BH, npiece): leaf block of each piece, -1 past the last
   int64_t seg_sum;     // int (BH, nseg): bucket counts per histogram scan segment
   int64_t dstar;       // int (L): reference causal mode: first uncorrected depth per query
+  int64_t logA;        // float (B, L, H, T + 1): exact causal with sparse levels, boundary log-masses
   int64_t total;
 };
 
@@ -539,6 +543,7 @@ struct BwdWorkspaceLayout {
   int64_t dsum;      // float (BH, NS, D)
   int64_t rc_coef;   // float (B, L, H, T): reference causal mode, boundary-mass gradient scale
   int64_t rc_rho;    // float (B, L, H, T): reference causal mode, on-path share of each boundary mass
+  int64_t rc_g;      // float (B, L, H, T): reference causal mode, boundary children's gradient (band depths)
   int64_t total;
 };
 

@@ -62,7 +62,8 @@ extern "C" int ta_forward_static(const ta_problem* p, const void* q, const void*
   Plan P;
   int rc = make_plan(p, &P);
   if (rc) return rc;
-  const int64_t per_bh = P.L * P.S * P.D * P.esize;  // partial rows of one (batch, head)
+  // pair rows of one (batch, head) (none for one-token leaves: their leaf stage is a value gather)
+  const int64_t per_bh = P.geo.LB == 1 ? 0 : P.L * P.S * P.D * P.esize;
   if (per_bh > kScratchBytes)
     return fail(TA_ERR_UNSUPPORTED,
                 "ta_forward_static: one (batch, head)'s pair rows take %lld bytes (L*num_samples*head_dim*%d), "
@@ -83,7 +84,7 @@ extern "C" int ta_forward_static(const ta_problem* p, const void* q, const void*
   if (rc) return rc;
   if (((uintptr_t)q | (uintptr_t)v | (uintptr_t)out | (uintptr_t)record | (need_k ? (uintptr_t)k : 0)) & 15)
     return fail(TA_ERR_INVALID, "q/k/v/out/record must be 16-byte aligned device pointers");
-  const int group = (int)(kScratchBytes / per_bh < P.BH ? kScratchBytes / per_bh : P.BH);
+  const int group = (int)(per_bh == 0 || kScratchBytes / per_bh >= P.BH ? P.BH : kScratchBytes / per_bh);
   for (int bh0 = 0; bh0 < P.BH; bh0 += group) {
     const int nbh = (int)(P.BH - bh0 < group ? P.BH - bh0 : group);
     hipError_t e = launch_leaf_fwd_group(P, q, k, v, out, (char*)record, scr, bh0, nbh, st);

@@ -17,6 +17,8 @@ struct Plan {
   int nseg;         // scan segments of the bucket histogram per (batch, head)
   int64_t Lp;       // L rounded up to a multiple of kQueryTile
   int qsplit;       // query splits of the summary-gradient product
+  int sample_dense; // the sampler's level tiles cover depths < sample_dense; deeper levels are sparse
+  int tree_dense;   // the backward's dense G tiles cover depths < tree_dense; deeper ones run in bands
   RecordLayout rec;
   FwdWorkspaceLayout fws;
   BwdWorkspaceLayout bws;
@@ -84,6 +86,12 @@ hipError_t launch_det_stream_bwd(int dtype, const void* q, const int64_t* qs, co
                                  const void* kn, const int64_t* ks, const void* v, const int64_t* vs, const float* lse,
                                  const float* delta, float* dq, float* achunk, float* dkn, void* dv,
                                  const int64_t* dvs, int B, int L, int H, int D, int T, int causal, hipStream_t st);
+
+// leaf_gather.hip (leaf_block 1: the leaf stage is a value gather)
+hipError_t launch_gather_fwd(const Plan& P, const void* v, void* out, const char* rec, int bh0, int nbh,
+                             hipStream_t st);
+hipError_t launch_gather_bwd(const Plan& P, const void* v, const void* g, void* dv, const char* rec, char* ws,
+                             hipStream_t st);
 
 // Leaf-kernel shared-memory need (bytes) for the chosen tile, or -1 if no
 // variant fits in 160 KiB.

@@ -622,6 +622,7 @@ static hipError_t leaf_bwd_d(const Plan& P, const void* q, const void* k, const 
 
 hipError_t launch_leaf_bwd(const Plan& P, const void* q, const void* k, const void* v, const void* g,
                            const char* rec, void* dv, char* ws, hipStream_t st) {
+  if (P.geo.LB == 1) return launch_gather_bwd(P, v, g, dv, rec, ws, st);
   switch (P.p.dtype) {
     case TA_F32: return leaf_bwd_d<float>(P, q, k, v, g, rec, dv, ws, st);
     case TA_BF16: return leaf_bwd_d<bf16>(P, q, k, v, g, rec, dv, ws, st);

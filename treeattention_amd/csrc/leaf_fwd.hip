@@ -431,6 +431,7 @@ static hipError_t leaf_fwd_d(const Plan& P, const void* q, const void* k, const 
 
 hipError_t launch_leaf_fwd_group(const Plan& P, const void* q, const void* k, const void* v, void* out, char* rec,
                                  void* partial, int bh0, int nbh, hipStream_t st) {
+  if (P.geo.LB == 1) return launch_gather_fwd(P, v, out, rec, bh0, nbh, st);
   switch (P.p.dtype) {
     case TA_F32: return leaf_fwd_d<float>(P, q, k, v, out, rec, partial, bh0, nbh, st);
     case TA_BF16: return leaf_fwd_d<bf16>(P, q, k, v, out, rec, partial, bh0, nbh, st);

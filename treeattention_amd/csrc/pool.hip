@@ -62,10 +62,41 @@ __global__ __launch_bounds__(256) void block_means_kernel(const E* __restrict__ 
   }
 }
 
+// Sums of aligned segments of kSeg block means (and of kSeg such segments),
+// so that a summary row over many blocks reads few rows: seg1[j] = sum of
+// means j kSeg .. (j + 1) kSeg - 1, seg2[j] = sum of seg1 rows likewise.
+// One thread per (segment, 8 dims); grid (ceil(nout D / 8 / 256), BH).
+constexpr int kSeg = 64;
+
+__global__ __launch_bounds__(256) void seg_sums_kernel(const float* __restrict__ in, int64_t nin_bh,
+                                                       float* __restrict__ out, int64_t nout_bh, int D) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nout_bh * (D / 8)) return;
+  const int bh = blockIdx.y;
+  const int64_t j = e / (D / 8);
+  const int d0 = (int)(e - j * (D / 8)) * 8;
+  const float* src = in + ((int64_t)bh * nin_bh + j * kSeg) * D + d0;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int t = 0; t < kSeg; t += 8) {
+    float x[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load8f(src + (int64_t)(t + u) * D, x[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += x[u][i];
+  }
+  float* o = out + ((int64_t)bh * nout_bh + j) * D + d0;
+  *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *(float4*)(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
 struct SumArgs {
   Geo geo;
   int H, D, mode;
   const float* means;   // (BH, NL, D)
+  const float* seg1;    // (BH, NL / kSeg, D) or null
+  const float* seg2;    // (BH, NL / kSeg^2, D) or null
   const void* knodes;   // node keys (node-keys mode)
   int64_t ksb, ksl, ksh;
   float* sum32;         // (BH, NS+pad, D)
@@ -73,6 +104,31 @@ struct SumArgs {
   void* sum_lo;         // E
   void* sum_t;          // E or float (BH, D, NS+pad)
 };
+
+// acc[0..8) += sum of block means [start, start + count) of this (batch, head)
+// (count a power of two, start a multiple of count), from the coarsest
+// segment sums that tile the range.
+__device__ __forceinline__ void sum_blocks(const SumArgs& a, int bh, int64_t start, int64_t count, int d0,
+                                           float* acc) {
+  const int D = a.D, NL = a.geo.NL;
+  const float* src = a.means + (int64_t)bh * NL * D;
+  int64_t n = count, s0 = start;
+  if (a.seg2 && count >= kSeg * kSeg) {
+    src = a.seg2 + (int64_t)bh * (NL / (kSeg * kSeg)) * D;
+    n = count / (kSeg * kSeg);
+    s0 = start / (kSeg * kSeg);
+  } else if (a.seg1 && count >= kSeg) {
+    src = a.seg1 + (int64_t)bh * (NL / kSeg) * D;
+    n = count / kSeg;
+    s0 = start / kSeg;
+  }
+  for (int64_t t = 0; t < n; ++t) {
+    float x[8];
+    load8f(src + (s0 + t) * D + d0, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += x[j];
+  }
+}
 
 // One workgroup per tile of 32 summary rows of one (batch, head); each
 // thread computes 8 dims of one row (vector loads of the block means), writes
@@ -100,13 +156,7 @@ __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
     if (i < G.pw[lam]) {  // rows past a level's b^lam nodes pad it to a multiple of 32
       if (a.mode == TA_TREE_NATURAL) {
         const int per = G.NL / G.pw[lam];
-        const float* m = a.means + ((int64_t)bh * G.NL + (int64_t)i * per) * D + d0;
-        for (int t = 0; t < per; ++t) {
-          float x[8];
-          load8f(m + (int64_t)t * D, x);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) val[j] += x[j];
-        }
+        sum_blocks(a, bh, (int64_t)i * per, per, d0, val);
         const float f = 0.5f / (float)per;
 #pragma unroll
         for (int j = 0; j < 8; ++j) val[j] *= f;
@@ -119,15 +169,9 @@ __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
         if (a.mode == TA_TREE_COMPAT) {
           const int p = n + 1;
           const int w = p & (-p);
-          const float* m = a.means + (int64_t)bh * G.NL * D + d0;
           float sl[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-          for (int t = 0; t < w; ++t) {
-            float xl[8], xr[8];
-            load8f(m + (int64_t)(p - w + t) * D, xl);
-            load8f(m + (int64_t)(p + t) * D, xr);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) { sl[j] += xl[j]; sr[j] += xr[j]; }
-          }
+          sum_blocks(a, bh, p - w, w, d0, sl);
+          sum_blocks(a, bh, p, w, d0, sr);
 #pragma unroll
           for (int j = 0; j < 8; ++j) coef[j] = 0.5f * (sl[j] - sr[j]) / (float)w;
         } else {
@@ -213,6 +257,20 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   a.sum_hi = rec + P.rec.sum_hi;
   a.sum_lo = rec + P.rec.sum_lo;
   a.sum_t = rec + P.rec.sum_t;
+  a.seg1 = a.seg2 = nullptr;
+  if (P.p.tree_mode != TA_TREE_NODEKEYS && G.NL >= 2 * kSeg) {
+    float* s1 = (float*)(rec + P.rec.segs);
+    const int64_t n1 = G.NL / kSeg, n2 = G.NL / (kSeg * kSeg);
+    hipLaunchKernelGGL(seg_sums_kernel, dim3((unsigned)((n1 * (P.D / 8) + 255) / 256), P.BH), dim3(256), 0, st,
+                       (const float*)means, (int64_t)G.NL, s1, n1, (int)P.D);
+    a.seg1 = s1;
+    if (n2 >= 2) {
+      float* s2 = s1 + P.BH * n1 * P.D;
+      hipLaunchKernelGGL(seg_sums_kernel, dim3((unsigned)((n2 * (P.D / 8) + 255) / 256), P.BH), dim3(256), 0, st,
+                         (const float*)s1, n1, s2, n2, (int)P.D);
+      a.seg2 = s2;
+    }
+  }
   if (G.NS > 0)
     hipLaunchKernelGGL(summaries_kernel<E>, dim3((unsigned)(G.NS / kSumRows), P.BH), dim3(256), 0, st, a);
   return hipGetLastError();

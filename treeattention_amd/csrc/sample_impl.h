@@ -46,6 +46,9 @@ struct SampleArgs {
   int* slot_count;
   const uint8_t* paths;  // replay: packed path bits (L, B, H, S, nbytes), else null
   int nbits, nbytes;
+  int Td;         // depths d >= Td are sparse: per-item child logits instead of level tiles
+  int pair_rows;  // binary compat / node-key trees: child rows +c, -c (one dot per node)
+  float* logA;    // causal, sparse levels: (B, L, H, T + 1) boundary log-masses between the kernels
 };
 
 constexpr int kLevelCols = 256;          // child columns of one level pass
@@ -201,6 +204,30 @@ __device__ __forceinline__ void row_dups16(int n, float e, int s, float& tot, bo
     row_dups16<R + 1>(n, e, s, tot, fst);
   }
 }
+// Lane j of each 16-lane row holds p[m] = its part of item m's sum (m < 16);
+// returns item j's total (sum over the row's lanes of p[j]), by halving
+// exchanges with lanes j ^ 8, j ^ 4, j ^ 2, j ^ 1.
+__device__ __forceinline__ float row_reduce_scatter16(const float (&p)[16], int j) {
+  float v8[8], v4[4], v2[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool up = j & 8;
+    v8[i] = (up ? p[i + 8] : p[i]) + __shfl_xor(up ? p[i] : p[i + 8], 8, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool up = j & 4;
+    v4[i] = (up ? v8[i + 4] : v8[i]) + __shfl_xor(up ? v8[i] : v8[i + 4], 4, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const bool up = j & 2;
+    v2[i] = (up ? v4[i + 2] : v4[i]) + __shfl_xor(up ? v4[i] : v4[i + 2], 2, 64);
+  }
+  const bool up = j & 1;
+  return (up ? v2[1] : v2[0]) + __shfl_xor(up ? v2[0] : v2[1], 1, 64);
+}
+
 // rank = number of row keys below n; cnt = number of row keys that are not
 // INT_MAX (this lane's included).
 template <int R = 0>
@@ -213,11 +240,333 @@ __device__ __forceinline__ void row_rank16(int key, int n, int& rank, int& cnt) 
   }
 }
 
+// Per-thread state of the root-to-leaf walks.  Items i = tid + 256 k map to
+// (query i / S, sample i % S); each item's node, log-prob, causal boundary leaf
+// block, uniforms' base index and (binary trees) last Philox block stay in
+// registers.  decide() takes one decision from the node's child logits,
+// finish() writes the weights and distinct leaf blocks; the dense-level kernel
+// and the sparse-level kernel share both.
+template <int kB, int kNI, bool kReplay>
+struct Walk {
+  static constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
+  int node[kNI], iq[kNI], is[kNI], iblk[kNI];
+  uint32_t rleaf[kNI];  // replay: the given leaf block of each item
+  int64_t ubase[kNI];
+  float acc[kNI];
+  RngCache rc[kNC];
+
+  __device__ __forceinline__ void init(const SampleArgs& a, int l0, int nq, int bb, int h, int tid) {
+    const Geo& G = a.geo;
+    const int S = a.S, T = G.T;
+    const int b = kB ? kB : G.b;
+    const int nitems = kQueryTile * S;
+#pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      const int it = tid + 256 * k;
+      node[k] = 0;
+      acc[k] = 0.f;
+      iq[k] = it < nitems ? it / S : kQueryTile;
+      is[k] = it < nitems ? it - iq[k] * S : 0;
+      if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
+      const int l = l0 + min(iq[k], nq - 1);
+      iblk[k] = (l + a.coff) / G.LB;
+      ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
+      rleaf[k] = 0u;
+      if (kReplay && iq[k] < kQueryTile)
+        rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * S + is[k]) * a.nbytes, a.nbits, a.nbytes);
+    }
+#pragma unroll
+    for (int k = 0; k < kNC; ++k) {
+      rc[k].ctr = ~0ull;
+      rc[k].w0 = rc[k].w1 = rc[k].w2 = rc[k].w3 = 0u;
+    }
+  }
+
+  // One decision of item k at depth d from its node's b child logits xr[0..b)
+  // (LDS for the dense passes, registers for the sparse levels); logA: the
+  // causal boundary log-masses [64][T+1].
+  __device__ __forceinline__ void decide(const SampleArgs& a, const float* logA, int k, int d, const float* xr) {
+    const Geo& G = a.geo;
+    const int T = G.T, lb = G.lb;
+    const int b = kB ? kB : G.b;
+    const int qi = iq[k];
+    const int shb = lb * (T - d), shc = lb * (T - 1 - d);
+    // log-sum-exp of the clamped child logits
+    float lse;
+    float x[kB ? kB : 1], ex[kB ? kB : 1];
+    if constexpr (kB != 0) {
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        x[j] = clampf(xr[j], a.maxhalf);
+        mx = fmaxf(mx, x[j]);
+      }
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        ex[j] = fast_exp2((x[j] - mx) * kLog2e);
+        se += ex[j];
+      }
+      lse = mx + fast_log2(se) * kLn2;
+    } else {
+      float mx = -__builtin_inff();
+      for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
+      float se = 0.f;
+      for (int j = 0; j < b; ++j) se += fast_exp2((clampf(xr[j], a.maxhalf) - mx) * kLog2e);
+      lse = mx + fast_log2(se) * kLn2;
+    }
+    if constexpr (kReplay) {  // the given digit, its log-prob (non-causal)
+      const int jr = (int)((rleaf[k] >> (lb * (T - 1 - d))) & (uint32_t)(b - 1));
+      float xj = 0.f;
+      if constexpr (kB != 0) {
+#pragma unroll
+        for (int j = 0; j < kB; ++j)
+          if (j == jr) xj = x[j];
+      } else {
+        xj = clampf(xr[jr], a.maxhalf);
+      }
+      node[k] = (node[k] << lb) + jr;
+      acc[k] += xj - lse;
+      return;
+    }
+    bool onb = false;
+    int js = 0;
+    float la_d = 0.f, la_c = 0.f;
+    if (a.causal && (iblk[k] >> shb) == node[k]) {
+      onb = true;
+      js = (iblk[k] >> shc) & (b - 1);
+      la_d = logA[qi * (T + 1) + d];
+      la_c = logA[qi * (T + 1) + d + 1];
+    }
+    const int64_t ub = ubase[k] + d * b;
+    if constexpr (kB != 0) {
+      // Gumbel-max in ratio form: lp_j - ln(-ln u_j) is, up to constants
+      // common to all children, ln(p_j / E_j) with E_j = -log2 u_j > 0,
+      // so the argmax is that of ex_j / E_j (ex_j = 2^((x_j - max) log2 e),
+      // proportional to p_j); on the boundary the allowed weights are
+      // ex_j (j < j*) and ex_j* A_{d+1}, rescaled to their own maximum.
+      float u[kB];
+      if constexpr (kB == 4) {  // the decision's four uniforms are one Philox block
+        if (a.U) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) u[j] = a.U[ub + j];
+        } else {
+          const Philox4 ph = philox4x32_10((uint64_t)ub >> 2, a.seed);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) u[j] = word_to_uniform(ph.w[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kB; ++j) u[j] = uniform_at(a.U, a.seed, ub + j, rc[kB == 2 ? k : 0]);
+      }
+      float wj[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) wj[j] = ex[j];
+      if (onb) {
+        float y[kB], my = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          y[j] = j < js ? x[j] * kLog2e : j == js ? x[j] * kLog2e + la_c * kLog2e : -__builtin_inff();
+          my = fmaxf(my, y[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kB; ++j) wj[j] = j <= js ? fast_exp2(y[j] - my) : 0.f;
+      }
+      float bw = wj[0], be = -fast_log2(u[0]);
+      int bj = 0;
+#pragma unroll
+      for (int j = 1; j < kB; ++j) {
+        const float e = -fast_log2(u[j]);
+        if (wj[j] * be > bw * e) {
+          bw = wj[j];
+          be = e;
+          bj = j;
+        }
+      }
+      float xb_ = x[0];
+#pragma unroll
+      for (int j = 1; j < kB; ++j)
+        if (j == bj) xb_ = x[j];
+      float lp = xb_ - lse;
+      if (onb) lp += bj < js ? -la_d : la_c - la_d;
+      node[k] = (node[k] << lb) + bj;
+      acc[k] += lp;
+      return;
+    }
+    RngCache local;
+    local.ctr = ~0ull;
+    local.w0 = local.w1 = local.w2 = local.w3 = 0u;
+    RngCache& cache = local;
+    float best = -__builtin_inff(), bl = 0.f;
+    int bj = 0;
+    auto consider = [&](int j, float xj) {
+      float lp = xj - lse;
+      if (onb) {
+        if (j < js) lp -= la_d;
+        else if (j == js) lp += la_c - la_d;
+        else lp = -__builtin_inff();
+      }
+      const float u = uniform_at(a.U, a.seed, ub + j, cache);
+      // lp + g up to the common constant -log(ln 2): g = -ln(ln2 * -log2 u)
+      const float sc = lp - kLn2 * fast_log2(-fast_log2(u));
+      if (sc > best) {
+        best = sc;
+        bj = j;
+        bl = lp;
+      }
+    };
+    for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
+    node[k] = (node[k] << lb) + bj;
+    acc[k] += bl;
+  }
+
+  // The walk's state between the dense-level and the sparse-level kernels:
+  // node and log-prob per item (in the record's leaf / slot-weight arrays,
+  // which finish() overwrites) and, causal, the boundary log-masses.
+  __device__ __forceinline__ void save(const SampleArgs& a, const float* logA, int l0, int nq, int bb, int h,
+                                       int tid) {
+    const int S = a.S, T1 = a.geo.T + 1;
+#pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      if (iq[k] >= kQueryTile) continue;
+      const int64_t o = (((int64_t)bb * a.L + l0 + iq[k]) * a.H + h) * S + is[k];
+      a.leaf[o] = node[k];
+      a.slot_weight[o] = acc[k];
+    }
+    if (a.causal)
+      for (int e = tid; e < nq * T1; e += 256) {
+        const int qi = e / T1, d = e - qi * T1;
+        a.logA[(((int64_t)bb * a.L + l0 + qi) * a.H + h) * T1 + d] = logA[qi * T1 + d];
+      }
+  }
+  __device__ __forceinline__ void load(const SampleArgs& a, float* logA, int l0, int nq, int bb, int h, int tid) {
+    const int S = a.S, T1 = a.geo.T + 1;
+#pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      if (iq[k] >= kQueryTile) continue;
+      const int64_t o = (((int64_t)bb * a.L + l0 + iq[k]) * a.H + h) * S + is[k];
+      node[k] = a.leaf[o];
+      acc[k] = a.slot_weight[o];
+    }
+    if (a.causal)
+      for (int e = tid; e < nq * T1; e += 256) {
+        const int qi = e / T1, d = e - qi * T1;
+        logA[qi * T1 + d] = a.logA[(((int64_t)bb * a.L + l0 + qi) * a.H + h) * T1 + d];
+      }
+  }
+
+  // Weights (softmax over the query's samples) and distinct leaf blocks;
+  // Xs: LDS scratch of at least 3 * 64 * S words.
+  __device__ __forceinline__ void finish(const SampleArgs& a, float* Xs, int l0, int bb, int h, int tid) {
+    const int S = a.S;
+    const int lane = tid & 63;
+    const int nitems = kQueryTile * S;
+    int* lf = (int*)Xs;
+    float* lps = Xs + kQueryTile * S;
+    int* fl = (int*)(Xs + 2 * kQueryTile * S);
+    // weights (softmax over the query's samples) and distinct leaf blocks
+    if (S == 16) {
+      // item tid + 256 k: a query's 16 samples are the 16 lanes of one DPP row
+      const int s = lane & 15;
+  #pragma unroll
+      for (int k = 0; k < kNI; ++k) {
+        const float m = row_max16(acc[k]);
+        const float e = fast_exp2((acc[k] - m) * kLog2e);
+        const float inv = 1.f / row_sum16(e);
+        float tot = e;  // weight of this leaf block summed over the samples from s on
+        bool fst = true;
+        row_dups16(node[k], e, s, tot, fst);
+        int rank = 0, cnt = 0;
+        row_rank16(fst ? node[k] : 0x7fffffff, node[k], rank, cnt);
+        const int qi = iq[k];
+        if (qi >= kQueryTile) continue;
+        const int l = l0 + qi;
+        const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+        a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = e * inv;
+        a.leaf[qh * S + s] = node[k];
+        if (fst) {
+          a.slot_leaf[qh * S + rank] = node[k];
+          a.slot_weight[qh * S + rank] = tot * inv;
+        }
+        if (s == 0) a.slot_count[qh] = cnt;
+      }
+      return;
+    }
+  #pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      const int it = tid + 256 * k;
+      if (it < nitems) {
+        lf[it] = node[k];
+        lps[it] = acc[k];
+      }
+    }
+    __syncthreads();
+    float wgt[kNI];
+    bool first[kNI];
+  #pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      wgt[k] = 0.f;
+      first[k] = false;
+      const int qi = iq[k];
+      if (qi >= kQueryTile) continue;
+      const int s = is[k];
+      const int* lq = lf + qi * S;
+      const float* pq = lps + qi * S;
+      float m = -__builtin_inff();
+      for (int j = 0; j < S; ++j) m = fmaxf(m, pq[j]);
+      float sum = 0.f, tot = 0.f;
+      bool fst = true;
+      for (int j = 0; j < S; ++j) {
+        const float e = fast_exp2((pq[j] - m) * kLog2e);
+        sum += e;
+        if (lq[j] == node[k]) {
+          if (j < s) fst = false;
+          else tot += e;
+        }
+      }
+      const float inv = 1.f / sum;
+      wgt[k] = fast_exp2((acc[k] - m) * kLog2e) * inv;
+      first[k] = fst;
+      acc[k] = tot * inv;  // summed weight of this leaf block (used if first)
+    }
+    // distinct-leaf keys: the leaf for a first occurrence, else INT_MAX
+  #pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      const int it = tid + 256 * k;
+      if (iq[k] < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
+      else if (it < nitems) fl[it] = 0x7fffffff;
+    }
+    __syncthreads();
+  #pragma unroll
+    for (int k = 0; k < kNI; ++k) {
+      const int qi = iq[k];
+      if (qi >= kQueryTile) continue;
+      const int s = is[k];
+      const int l = l0 + qi;
+      const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+      a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = wgt[k];
+      a.leaf[qh * S + s] = node[k];
+      const int* fq = fl + qi * S;
+      if (first[k]) {
+        int rank = 0;
+        for (int j = 0; j < S; ++j) rank += fq[j] < node[k];
+        a.slot_leaf[qh * S + rank] = node[k];
+        a.slot_weight[qh * S + rank] = acc[k];
+      }
+      if (s == 0) {
+        int cnt = 0;
+        for (int j = 0; j < S; ++j) cnt += fq[j] != 0x7fffffff;
+        a.slot_count[qh] = cnt;
+      }
+    }
+  }
+};
+
 // kB: branching known at compile time (2 or 4), or 0 for the runtime value.
 // kNI: (query, sample) items per thread, >= 64 * S / 256.
 // kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
 template <typename E, int D, int kB, int kNI, bool kReplay>
-__global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
+__global__ __launch_bounds__(256, 2) void sample_kernel(SampleArgs a) {
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
@@ -232,10 +581,7 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   float* Xs = (float*)smem;                      // [64][kXS] logits of one level pass
   float* logA = Xs + kQueryTile * kXS;           // [64][T+1] causal boundary log-mass
   float* xb = logA + kQueryTile * (T + 1);       // [64][T*b] boundary child logits
-  // after the walk Xs is reused: leaf, log-prob and distinct-leaf key per item
-  int* lf = (int*)Xs;
-  float* lps = Xs + kQueryTile * S;
-  int* fl = (int*)(Xs + 2 * kQueryTile * S);
+  // after the walk Xs is reused by finish()
 
   // all 64 query rows as MFMA B fragments (rows past nq are zero)
   RowFrags<E, D> qa[4];
@@ -261,36 +607,8 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     for (int d = 0; d < T; ++d) ps.nbt += ps.btiles(d);
   const int nbatch = ps.causal ? ps.nbatch() : 0;
 
-  // items: i = tid + 256 k -> (query i / S, sample i % S); node, log-prob,
-  // the causal boundary leaf block, the uniforms' base index and (binary
-  // trees) the last Philox block stay in registers
-  const int nitems = kQueryTile * S;
-  int node[kNI], iq[kNI], is[kNI], iblk[kNI];
-  uint32_t rleaf[kNI];  // replay: the given leaf block of each item
-  int64_t ubase[kNI];
-  float acc[kNI];
-  constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
-  RngCache rc[kNC];
-#pragma unroll
-  for (int k = 0; k < kNI; ++k) {
-    const int it = tid + 256 * k;
-    node[k] = 0;
-    acc[k] = 0.f;
-    iq[k] = it < nitems ? it / S : kQueryTile;
-    is[k] = it < nitems ? it - iq[k] * S : 0;
-    if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
-    const int l = l0 + min(iq[k], nq - 1);
-    iblk[k] = (l + a.coff) / G.LB;
-    ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
-    rleaf[k] = 0u;
-    if (kReplay && iq[k] < kQueryTile)
-      rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * S + is[k]) * a.nbytes, a.nbits, a.nbytes);
-  }
-#pragma unroll
-  for (int k = 0; k < kNC; ++k) {
-    rc[k].ctr = ~0ull;
-    rc[k].w0 = rc[k].w1 = rc[k].w2 = rc[k].w3 = 0u;
-  }
+  Walk<kB, kNI, kReplay> wk;
+  wk.init(a, l0, nq, bb, h, tid);
 
   // pass p < nbatch: causal boundary batch p; then level d, chunk c0
   LogitPipe<E, D, kLo> pipe;
@@ -313,9 +631,10 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
   // node >= c0 of the next depth, whose children (>= 2 c0) lie past every
   // later pass of the level, so no item decides twice in one level.
   auto last_c0 = [&](int dd) { return (ps.level_cols(dd) - 1) / kLevelCols * kLevelCols; };
+  const int Td = a.Td;  // dense levels 0 .. Td - 1
   int p = 0, d = 0, c0 = 0;  // current pass (level 0 has b <= kLevelCols children)
-  if (T > 0) prefetch(0, 0, 0);
-  while (p < nbatch || d < T) {
+  if (nbatch > 0 || Td > 0) prefetch(0, 0, 0);
+  while (p < nbatch || d < Td) {
     const int nt = tiles_of(p, d, c0);
     if (p < nbatch) {
       const int t0 = p * (kLevelCols / 16);
@@ -332,10 +651,10 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
         nc0 = c0 - kLevelCols;
       } else {
         ++nd;
-        nc0 = nd < T ? last_c0(nd) : 0;
+        nc0 = nd < Td ? last_c0(nd) : 0;
       }
     }
-    if (np < nbatch || nd < T) prefetch(np, nd, nc0);
+    if (np < nbatch || nd < Td) prefetch(np, nd, nc0);
 
     if (p < nbatch) {
       // boundary child logits of this batch's depths: query tid & 63, depths
@@ -396,141 +715,13 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
       }
     } else {
       const int ncols = min(kLevelCols, ps.level_cols(d) - c0);
-      const int shb = lb * (T - d), shc = lb * (T - 1 - d);
 #pragma unroll
       for (int k = 0; k < kNI; ++k) {
-        const int qi = iq[k];
+        const int qi = wk.iq[k];
         if (qi >= kQueryTile) continue;
-        const int base = (node[k] << lb) - c0;
+        const int base = (wk.node[k] << lb) - c0;
         if (base < 0 || base >= ncols) continue;
-        const float* xr = Xs + qi * kXS + base;
-        // log-sum-exp of the clamped child logits
-        float lse;
-        float x[kB ? kB : 1], ex[kB ? kB : 1];
-        if constexpr (kB != 0) {
-          float mx = -__builtin_inff();
-#pragma unroll
-          for (int j = 0; j < kB; ++j) {
-            x[j] = clampf(xr[j], a.maxhalf);
-            mx = fmaxf(mx, x[j]);
-          }
-          float se = 0.f;
-#pragma unroll
-          for (int j = 0; j < kB; ++j) {
-            ex[j] = fast_exp2((x[j] - mx) * kLog2e);
-            se += ex[j];
-          }
-          lse = mx + fast_log2(se) * kLn2;
-        } else {
-          float mx = -__builtin_inff();
-          for (int j = 0; j < b; ++j) mx = fmaxf(mx, clampf(xr[j], a.maxhalf));
-          float se = 0.f;
-          for (int j = 0; j < b; ++j) se += fast_exp2((clampf(xr[j], a.maxhalf) - mx) * kLog2e);
-          lse = mx + fast_log2(se) * kLn2;
-        }
-        if constexpr (kReplay) {  // the given digit, its log-prob (non-causal)
-          const int jr = (int)((rleaf[k] >> (lb * (T - 1 - d))) & (uint32_t)(b - 1));
-          float xj = 0.f;
-          if constexpr (kB != 0) {
-#pragma unroll
-            for (int j = 0; j < kB; ++j)
-              if (j == jr) xj = x[j];
-          } else {
-            xj = clampf(xr[jr], a.maxhalf);
-          }
-          node[k] = (node[k] << lb) + jr;
-          acc[k] += xj - lse;
-          continue;
-        }
-        bool onb = false;
-        int js = 0;
-        float la_d = 0.f, la_c = 0.f;
-        if (a.causal && (iblk[k] >> shb) == node[k]) {
-          onb = true;
-          js = (iblk[k] >> shc) & (b - 1);
-          la_d = logA[qi * (T + 1) + d];
-          la_c = logA[qi * (T + 1) + d + 1];
-        }
-        const int64_t ub = ubase[k] + d * b;
-        if constexpr (kB != 0) {
-          // Gumbel-max in ratio form: lp_j - ln(-ln u_j) is, up to constants
-          // common to all children, ln(p_j / E_j) with E_j = -log2 u_j > 0,
-          // so the argmax is that of ex_j / E_j (ex_j = 2^((x_j - max) log2 e),
-          // proportional to p_j); on the boundary the allowed weights are
-          // ex_j (j < j*) and ex_j* A_{d+1}, rescaled to their own maximum.
-          float u[kB];
-          if constexpr (kB == 4) {  // the decision's four uniforms are one Philox block
-            if (a.U) {
-#pragma unroll
-              for (int j = 0; j < 4; ++j) u[j] = a.U[ub + j];
-            } else {
-              const Philox4 ph = philox4x32_10((uint64_t)ub >> 2, a.seed);
-#pragma unroll
-              for (int j = 0; j < 4; ++j) u[j] = word_to_uniform(ph.w[j]);
-            }
-          } else {
-#pragma unroll
-            for (int j = 0; j < kB; ++j) u[j] = uniform_at(a.U, a.seed, ub + j, rc[kB == 2 ? k : 0]);
-          }
-          float wj[kB];
-#pragma unroll
-          for (int j = 0; j < kB; ++j) wj[j] = ex[j];
-          if (onb) {
-            float y[kB], my = -__builtin_inff();
-#pragma unroll
-            for (int j = 0; j < kB; ++j) {
-              y[j] = j < js ? x[j] * kLog2e : j == js ? x[j] * kLog2e + la_c * kLog2e : -__builtin_inff();
-              my = fmaxf(my, y[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < kB; ++j) wj[j] = j <= js ? fast_exp2(y[j] - my) : 0.f;
-          }
-          float bw = wj[0], be = -fast_log2(u[0]);
-          int bj = 0;
-#pragma unroll
-          for (int j = 1; j < kB; ++j) {
-            const float e = -fast_log2(u[j]);
-            if (wj[j] * be > bw * e) {
-              bw = wj[j];
-              be = e;
-              bj = j;
-            }
-          }
-          float xb_ = x[0];
-#pragma unroll
-          for (int j = 1; j < kB; ++j)
-            if (j == bj) xb_ = x[j];
-          float lp = xb_ - lse;
-          if (onb) lp += bj < js ? -la_d : la_c - la_d;
-          node[k] = (node[k] << lb) + bj;
-          acc[k] += lp;
-          continue;
-        }
-        RngCache local;
-        local.ctr = ~0ull;
-        local.w0 = local.w1 = local.w2 = local.w3 = 0u;
-        RngCache& cache = local;
-        float best = -__builtin_inff(), bl = 0.f;
-        int bj = 0;
-        auto consider = [&](int j, float xj) {
-          float lp = xj - lse;
-          if (onb) {
-            if (j < js) lp -= la_d;
-            else if (j == js) lp += la_c - la_d;
-            else lp = -__builtin_inff();
-          }
-          const float u = uniform_at(a.U, a.seed, ub + j, cache);
-          // lp + g up to the common constant -log(ln 2): g = -ln(ln2 * -log2 u)
-          const float sc = lp - kLn2 * fast_log2(-fast_log2(u));
-          if (sc > best) {
-            best = sc;
-            bj = j;
-            bl = lp;
-          }
-        };
-        for (int j = 0; j < b; ++j) consider(j, clampf(xr[j], a.maxhalf));
-        node[k] = (node[k] << lb) + bj;
-        acc[k] += bl;
+        wk.decide(a, logA, k, d, Xs + qi * kXS + base);
       }
     }
     __syncthreads();
@@ -539,101 +730,99 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     c0 = nc0;
   }
 
-  // weights (softmax over the query's samples) and distinct leaf blocks
-  if (S == 16) {
-    // item tid + 256 k: a query's 16 samples are the 16 lanes of one DPP row
-    const int s = lane & 15;
-#pragma unroll
-    for (int k = 0; k < kNI; ++k) {
-      const float m = row_max16(acc[k]);
-      const float e = fast_exp2((acc[k] - m) * kLog2e);
-      const float inv = 1.f / row_sum16(e);
-      float tot = e;  // weight of this leaf block summed over the samples from s on
-      bool fst = true;
-      row_dups16(node[k], e, s, tot, fst);
-      int rank = 0, cnt = 0;
-      row_rank16(fst ? node[k] : 0x7fffffff, node[k], rank, cnt);
-      const int qi = iq[k];
-      if (qi >= kQueryTile) continue;
-      const int l = l0 + qi;
-      const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-      a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = e * inv;
-      a.leaf[qh * S + s] = node[k];
-      if (fst) {
-        a.slot_leaf[qh * S + rank] = node[k];
-        a.slot_weight[qh * S + rank] = tot * inv;
-      }
-      if (s == 0) a.slot_count[qh] = cnt;
-    }
+
+  if (Td < T) {  // the sparse-level kernel continues the walks
+    wk.save(a, logA, l0, nq, bb, h, tid);
     return;
   }
+  wk.finish(a, Xs, l0, bb, h, tid);
+}
+
+// The sparse levels (d >= Td, wider than level tiles pay for), continuing the
+// walks the dense-level kernel saved: each item's child logits are dot
+// products of its query row with its node's child summary rows (float).  The
+// 16 lanes of a DPP row take the row's 16 items in turn, lane j covering head
+// dims [DPL j, DPL (j + 1)) (one coalesced 16 * DPL-float piece of the
+// summary row per item), then a reduce-scatter over the row leaves each lane
+// its own item's logits.  Cost per item and level: b summary rows (compat /
+// node-key trees: 1), linear in L.  Same grid and LDS as sample_kernel.
+template <typename E, int D, int kB, int kNI, bool kReplay>
+__global__ __launch_bounds__(256) void sample_sparse_kernel(SampleArgs a) {
+  static_assert(kB == 2 || kB == 4, "sparse levels: b = 2 or 4");
+  extern __shared__ __align__(16) char smem[];
+  const Geo& G = a.geo;
+  const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int l0 = blockIdx.x * kQueryTile;
+  const int nq = min(kQueryTile, a.L - l0);
+  const int T = G.T, Td = a.Td;
+  const int tid = threadIdx.x, lane = tid & 63;
+  float* Xs = (float*)smem;                 // [64][D + 4] query rows, then finish()'s arrays
+  float* logA = Xs + kQueryTile * kXS;      // [64][T+1]
+  Walk<kB, kNI, kReplay> wk;
+  wk.init(a, l0, nq, bb, h, tid);
+  wk.load(a, logA, l0, nq, bb, h, tid);
+  {
+    constexpr int QS = D + 4;
+    float* qs = Xs;  // [64][QS] float query rows (the logit tile is free now)
+    for (int e = tid; e < kQueryTile * (D / 8); e += 256) {
+      const int r = e / (D / 8), c = (e - r * (D / 8)) * 8;
+      float v8[8];
 #pragma unroll
-  for (int k = 0; k < kNI; ++k) {
-    const int it = tid + 256 * k;
-    if (it < nitems) {
-      lf[it] = node[k];
-      lps[it] = acc[k];
+      for (int i = 0; i < 8; ++i) v8[i] = 0.f;
+      if (r < nq) {
+        const E* src = (const E*)a.q + bb * a.qsb + (int64_t)(l0 + r) * a.qsl + h * a.qsh + c;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v8[i] = tof(src[i]);
+      }
+      *(float4*)(qs + r * QS + c) = make_float4(v8[0], v8[1], v8[2], v8[3]);
+      *(float4*)(qs + r * QS + c + 4) = make_float4(v8[4], v8[5], v8[6], v8[7]);
     }
-  }
-  __syncthreads();
-  float wgt[kNI];
-  bool first[kNI];
+    __syncthreads();
+    constexpr int DPL = D / 16;  // head dims per lane: 2, 4, 6 or 8
+    const int j16 = lane & 15, r0 = lane & 48;
+    const int nrow = a.pair_rows ? 1 : kB;
+    for (int dd = Td; dd < T; ++dd) {
+      const float* lvl = a.sum32 + ((int64_t)bh * G.NS + G.off[dd + 1]) * D + DPL * j16;
 #pragma unroll
-  for (int k = 0; k < kNI; ++k) {
-    wgt[k] = 0.f;
-    first[k] = false;
-    const int qi = iq[k];
-    if (qi >= kQueryTile) continue;
-    const int s = is[k];
-    const int* lq = lf + qi * S;
-    const float* pq = lps + qi * S;
-    float m = -__builtin_inff();
-    for (int j = 0; j < S; ++j) m = fmaxf(m, pq[j]);
-    float sum = 0.f, tot = 0.f;
-    bool fst = true;
-    for (int j = 0; j < S; ++j) {
-      const float e = fast_exp2((pq[j] - m) * kLog2e);
-      sum += e;
-      if (lq[j] == node[k]) {
-        if (j < s) fst = false;
-        else tot += e;
+      for (int k = 0; k < kNI; ++k) {
+        float part[kB][16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          const int qm = __shfl(wk.iq[k], r0 + m, 64);
+          const int nm = __shfl(wk.node[k], r0 + m, 64);
+          const bool act = qm < kQueryTile;
+          const float* qrow = qs + (act ? qm : 0) * QS + DPL * j16;
+          float qv[DPL];
+#pragma unroll
+          for (int i = 0; i < DPL; i += 2) {
+            const float2 t = *(const float2*)(qrow + i);
+            qv[i] = t.x;
+            qv[i + 1] = t.y;
+          }
+#pragma unroll
+          for (int j = 0; j < kB; ++j) {
+            float sacc = 0.f;
+            if (j < nrow) {
+              const float* crow = lvl + ((int64_t)(act ? nm : 0) * kB + j) * D;
+#pragma unroll
+              for (int i = 0; i < DPL; i += 2) {
+                const float2 t = *(const float2*)(crow + i);
+                sacc += qv[i] * t.x + qv[i + 1] * t.y;
+              }
+            }
+            part[j][m] = sacc;
+          }
+        }
+        float xo[kB];
+#pragma unroll
+        for (int j = 0; j < kB; ++j) xo[j] = row_reduce_scatter16(part[j], j16);
+        if (a.pair_rows) xo[1] = -xo[0];
+        if (wk.iq[k] < kQueryTile) wk.decide(a, logA, k, dd, xo);
       }
     }
-    const float inv = 1.f / sum;
-    wgt[k] = fast_exp2((acc[k] - m) * kLog2e) * inv;
-    first[k] = fst;
-    acc[k] = tot * inv;  // summed weight of this leaf block (used if first)
+    __syncthreads();  // qs (Xs) is reused below
   }
-  // distinct-leaf keys: the leaf for a first occurrence, else INT_MAX
-#pragma unroll
-  for (int k = 0; k < kNI; ++k) {
-    const int it = tid + 256 * k;
-    if (iq[k] < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
-    else if (it < nitems) fl[it] = 0x7fffffff;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kNI; ++k) {
-    const int qi = iq[k];
-    if (qi >= kQueryTile) continue;
-    const int s = is[k];
-    const int l = l0 + qi;
-    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = wgt[k];
-    a.leaf[qh * S + s] = node[k];
-    const int* fq = fl + qi * S;
-    if (first[k]) {
-      int rank = 0;
-      for (int j = 0; j < S; ++j) rank += fq[j] < node[k];
-      a.slot_leaf[qh * S + rank] = node[k];
-      a.slot_weight[qh * S + rank] = acc[k];
-    }
-    if (s == 0) {
-      int cnt = 0;
-      for (int j = 0; j < S; ++j) cnt += fq[j] != 0x7fffffff;
-      a.slot_count[qh] = cnt;
-    }
-  }
+  wk.finish(a, Xs, l0, bb, h, tid);
 }
 
 // Xs (which the final phase's three [64][S] arrays alias: 3 * 64 * 64 * 4
@@ -675,6 +864,9 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.slot_leaf = (int*)(rec + P.rec.slot_leaf);
   a.slot_weight = (float*)(rec + P.rec.slot_weight);
   a.slot_count = (int*)(rec + P.rec.slot_count);
+  a.Td = P.sample_dense;
+  a.pair_rows = P.p.tree_mode != TA_TREE_NATURAL && P.geo.b == 2;
+  a.logA = (float*)(rec + P.rec.logA);
   const int smem = sample_smem(P);
   auto launch = [&](auto kern) -> hipError_t {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
@@ -682,7 +874,10 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
     hipLaunchKernelGGL(kern, dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH), dim3(256), smem, st, a);
     return hipGetLastError();
   };
-  return launch(sample_kernel<E, D, kB, kNI, kReplay>);
+  hipError_t e = launch(sample_kernel<E, D, kB, kNI, kReplay>);
+  if constexpr (kB == 2 || kB == 4)
+    if (e == hipSuccess && P.sample_dense < P.geo.T) e = launch(sample_sparse_kernel<E, D, kB, kNI, kReplay>);
+  return e;
 }
 
 template <bool kReplay, typename E, int D>

@@ -65,6 +65,12 @@ struct TreeArgs {
   const int* dstar;       // (L) first uncorrected depth per query
   float* rc_coef;         // (B, L, H, T)
   float* rc_rho;          // (B, L, H, T)
+  float* rc_g;            // (B, L, H, T): the boundary children's gradient g (left +g, right -g) per depth
+  // levels d < Tb are dense (G tiles; G^T rows 0 .. nsd - 1 per query tile); deeper ones
+  // are the band kernels' (tree_band_kernel)
+  int Tb, nsd;
+  int dqp;  // 1: add each query's per-pair dq rows (leaf dq and deep-level tree dq)
+  int dkl;  // 1: add the leaf part of dk
 };
 
 template <typename E>
@@ -129,9 +135,11 @@ __global__ __launch_bounds__(256) void ref_causal_grad_kernel(TreeArgs a) {
   const int t = (int)(bl % L), bb = (int)(bl / L);
   float* cf = a.rc_coef + gid * T;
   float* rh = a.rc_rho + gid * T;
+  float* gg = a.rc_g + gid * T;
   for (int d = 0; d < T; ++d) {
     cf[d] = 0.f;
     rh[d] = 0.f;
+    gg[d] = 0.f;
   }
   if (t < a.t0) return;
   const int ds = a.dstar[t];
@@ -165,6 +173,15 @@ __global__ __launch_bounds__(256) void ref_causal_grad_kernel(TreeArgs a) {
   for (int d = ds; d < T; ++d) {
     cf[d] = A * gam;
     gam *= rh[d];
+  }
+  // the gradient of the boundary node's left child logit at depth d,
+  // g = coef_d (rho_left - p_left) (the right child gets -g); the dense
+  // levels add it to G in tree_dq_kernel, the band levels through rc_g
+  for (int d = max(ds, a.Tb); d < T; ++d) {
+    const float* crow = a.sum32 + ((int64_t)bh * a.geo.NS + a.geo.off[d + 1] + 2 * (c >> (T - d))) * D;
+    const float pl = 1.f / (1.f + __expf(-2.f * dot_row(qr, crow, D)));
+    const float rl = ((c >> (T - 1 - d)) & 1) ? 1.f - rh[d] : rh[d];
+    gg[d] = cf[d] * (rl - pl);
   }
 }
 
@@ -570,12 +587,13 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       }
     }
   };
+  const int Tb = a.Tb;  // dense depths 0 .. Tb - 1
   int d = 0, c0 = 0;
-  if (T > 0) {
+  if (Tb > 0) {
     load_af(0, 0);
     load_at(0, 0);
   }
-  while (d < T) {
+  while (d < Tb) {
     const int lam = d + 1, lvl = G.pw[lam];
     const int ncols = min(kChunk, lvl - c0);
     const int rcols = max(0, min(ncols, reach(d) - c0));  // columns that can be nonzero
@@ -607,7 +625,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     for (int i = 0; i < NMD; ++i)
 #pragma unroll
       for (int ks = 0; ks < KT; ++ks) asm volatile("" ::"v"(at[i][ks]) : "memory");
-    if (nd < T) load_af(nd, nc0);
+    if (nd < Tb) load_af(nd, nc0);
     for (int e = tid; e < kQueryTile * rk / 8; e += 256) {
       const int r = e / (rk / 8), cc = (e - r * (rk / 8)) * 8;
       z8(sm.Gm + r * kGS + cc);
@@ -647,7 +665,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
       // G^T rows of the chunk up to the reach (without the causal restriction
       // rk covers the chunk rounded up to 32 rows, the level's zero padding
       // included), eight queries per 16-byte store
-      E* gt = (E*)a.gt + (((int64_t)bh * gridDim.x + blockIdx.x) * rows + G.off[lam] + c0) * kQueryTile;
+      E* gt = (E*)a.gt + (((int64_t)bh * gridDim.x + blockIdx.x) * a.nsd + G.off[lam] + c0) * kQueryTile;
       for (int e = tid; e < rk * (kQueryTile / 8); e += 256) {
         const int cc = e >> 3, q0 = (e & 7) * 8;
         E v8[8];
@@ -673,7 +691,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
         }
       }
     }
-    if (nd < T) load_at(nd, nc0);
+    if (nd < Tb) load_at(nd, nc0);
     __syncthreads();
     d = nd;
     c0 = nc0;
@@ -699,7 +717,18 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = stage[qi * SS + d0 + i];
-    sum_rows8(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
+    if (a.dqp) sum_rows8(acc, dqp + qh * S * D + d0, D, sm.cn[qi]);
+    if (a.refc && Tb < T) {
+      // boundary-mass gradient at the band depths: dq += g (c_left - c_right) = 2 g c_left
+      for (int dd = Tb; dd < T; ++dd) {
+        const float gv = a.rc_g[qh * T + dd];
+        if (gv == 0.f) continue;
+        const float* cl = a.sum32 + ((int64_t)bh * rows + G.off[dd + 1] + 2 * (l >> (T - dd))) * D + d0;
+        const float4 x0 = *(const float4*)cl, x1 = *(const float4*)(cl + 4);
+        acc[0] += 2.f * gv * x0.x; acc[1] += 2.f * gv * x0.y; acc[2] += 2.f * gv * x0.z; acc[3] += 2.f * gv * x0.w;
+        acc[4] += 2.f * gv * x1.x; acc[5] += 2.f * gv * x1.y; acc[6] += 2.f * gv * x1.z; acc[7] += 2.f * gv * x1.w;
+      }
+    }
     E* o = dq + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + d0;
     if constexpr (sizeof(E) == 2) {
       typedef __attribute__((ext_vector_type(8))) E e8;
@@ -739,7 +768,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   __shared__ __align__(16) E qs[2][D * QS];
   const int chunk = blockIdx.x, split = blockIdx.y, bh = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
-  const int rows = a.geo.NS, ntile = rows / 16;
+  const int rows = a.nsd, ntile = rows / 16;  // the dense levels' rows
   const int64_t Lp = a.Lp;
   const int64_t nblk = Lp / kDcKB, qs_ = a.qsplit;
   const int64_t nj = split < nblk ? (nblk - split + qs_ - 1) / qs_ : 0;  // this split's query blocks
@@ -867,18 +896,19 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
   }
 }
 
-// dsum = sum over query splits (in split order); rows outside any level are 0.
+// dsum rows of the dense levels (the first nsd rows of each (batch, head)) =
+// sum over query splits (in split order); rows outside any level are 0.
 __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restrict__ part, float* __restrict__ dsum,
-                                                          int64_t n, int qsplit, Geo G, int D) {
+                                                          int64_t n, int qsplit, Geo G, int D, int nsd) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= n) return;
-  const int64_t r = (e / D) % G.NS;
+  const int64_t row = e / D, bh = row / nsd, r = row - bh * nsd;
   int lam = 1;
   while (lam < G.T && r >= G.off[lam + 1]) ++lam;
   float s = 0.f;
   if (r - G.off[lam] < G.pw[lam])
     for (int k = 0; k < qsplit; ++k) s += part[(int64_t)k * n + e];
-  dsum[e] = s;
+  dsum[(bh * G.NS + r) * D + (e - row * D)] = s;
 }
 
 // dk[b, t, h, :] = dk_leaf + sum over the summaries that include token t.
@@ -928,8 +958,12 @@ __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
   }
   const float inv = 1.f / (float)G.LB;
   const int64_t th = ((int64_t)bb * a.N + t) * a.H + h;
-  const float4* lk = (const float4*)(a.dk_leaf + th * D + d0);
-  const float4 l0 = lk[0], l1 = lk[1];
+  float4 l0 = make_float4(0.f, 0.f, 0.f, 0.f), l1 = l0;
+  if (a.dkl) {
+    const float4* lk = (const float4*)(a.dk_leaf + th * D + d0);
+    l0 = lk[0];
+    l1 = lk[1];
+  }
   const float r[8] = {l0.x + acc[0] * inv, l0.y + acc[1] * inv, l0.z + acc[2] * inv, l0.w + acc[3] * inv,
                       l1.x + acc[4] * inv, l1.y + acc[5] * inv, l1.z + acc[6] * inv, l1.w + acc[7] * inv};
   E* o = (E*)a.dk + bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d0;
@@ -960,6 +994,281 @@ __global__ __launch_bounds__(256) void nodekeys_adjoint_kernel(TreeArgs a) {
   const int64_t rl = G.off[dep + 1] + 2 * ip;
   const float* ds = a.dsum + (int64_t)bh * G.NS * D + d;
   ((E*)a.dk)[bb * a.ksb + (int64_t)nn * a.ksl + h * a.ksh + d] = (E)(0.5f * (ds[rl * D] - ds[(rl + 1) * D]));
+}
+
+// ---------------------------------------------------------------- bands ---
+// The deep levels (depths Tb .. T-1, wider than dense G tiles pay for) run in
+// bands of nb depths [da, da + nb), linear in the number of sampled pairs.  A
+// band's work under node s of depth da is one workgroup: the subtree's
+// (query, distinct leaf block) pairs are one contiguous run of the bucket
+// order (pairs sorted by leaf block are sorted by node at every depth), taken
+// 64 at a time, four threads per pair.  At depth d of the band the query's
+// slots under the pair's node n form a run, and its first slot (the run's
+// representative) carries the node's entries of G:
+//   G[n, j] = A_j - p_j A_n
+// (A_j: dl summed over the run's slots under child j, A_n over the run, p the
+// node's child probabilities from x_j = q . c_{n,j} with the float summaries,
+// 0 where the logit is clamped), exactly the dense levels' rule.  Then
+//   dq_pair += sum_j G[n, j] c_{n,j}  (into the pair's dq row, summed per query
+//                                      by tree_dq_kernel's epilogue),
+//   dC_sub  += G_tile^T Q_tile        (MFMA over the tile's 64 pairs),
+// and the subtree's R band rows of dC are written once at the end: one writer
+// per entry and a fixed summation order, no atomics.
+struct BandArgs {
+  Geo geo;
+  int L, H, S, da, nb, R, pair_rows, rmw;
+  float maxhalf;
+  const void* q;
+  int64_t qsb, qsl, qsh;
+  const float* sum32;
+  const int* slot_leaf;
+  const int* slot_count;
+  const float* dl;
+  const int* order;
+  const int* block_start;
+  void* dq_part;
+  float* dsum;
+};
+
+constexpr int kBandRows = 64;  // dC rows of one band's subtree (b = 2: 5 depths, b = 4: 2)
+
+template <typename E>
+__device__ __forceinline__ void ld8f(float* o, const E* p) {
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(8))) E e8;
+    const e8 v = *(const e8*)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (float)v[i];
+  } else {
+    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
+    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+  }
+}
+
+template <typename E, int D, int kB>
+__global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
+  using M = Mfma<E>;
+  using F = typename M::frag;
+  constexpr int DQ = D / 4;  // head dims per thread
+  constexpr int lb = kB == 2 ? 1 : 2;
+  constexpr int GS = 64 + (sizeof(E) == 2 ? 8 : 4);  // G tile row stride (elements)
+  constexpr int QS = D + (sizeof(E) == 2 ? 8 : 4);   // Q tile row stride
+  constexpr int NCT = D / 16;
+  constexpr int NT = (kBandRows / 16) * NCT;  // output tiles at most
+  constexpr int TPW = (NT + 3) / 4;
+  __shared__ __align__(16) E Gt[kBandRows * GS];  // [band row][pair]
+  __shared__ __align__(16) E Qs[64 * QS];         // [pair][dim]
+  const Geo& G = a.geo;
+  const int s0 = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
+  const int tp = tid >> 2, tq = tid & 3;
+  const int T = G.T, S = a.S, da = a.da, nb = a.nb, R = a.R;
+  const int RP = (R + 15) & ~15, ntu = (RP / 16) * NCT;
+  const int span = 1 << (lb * (T - da));  // leaf blocks under the subtree
+  const int* bs = a.block_start + (int64_t)bh * (G.NL + 1);
+  const int e_begin = bs[s0 * span], e_end = bs[(s0 + 1) * span];
+  const int* ord = a.order + (int64_t)bh * a.L * S;
+  const float* sum = a.sum32 + (int64_t)bh * G.NS * D;
+
+  f32x4 acc[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) acc[k] = zero4();
+  for (int e0 = e_begin; e0 < e_end; e0 += 64) {
+    for (int e = tid; e < RP * 64; e += 256) Gt[(e >> 6) * GS + (e & 63)] = (E)0.f;
+    const int e = e0 + tp;
+    const bool valid = e < e_end;
+    const int ent = valid ? ord[e] : 0;
+    const int l = ent / S, u = ent - l * S;
+    const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
+    const int* sl = a.slot_leaf + qh * S;
+    const float* dls = a.dl + qh * S;
+    const int cnt = valid ? a.slot_count[qh] : 0;
+    const int leaf = valid ? sl[u] : 0;
+    float qv[DQ];
+    const E* qr = (const E*)a.q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + tq * DQ;
+#pragma unroll
+    for (int i = 0; i < DQ; i += 8) {
+      if (valid) ld8f(qv + i, qr + i);
+      else
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qv[i + t] = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) Qs[tp * QS + tq * DQ + i + t] = (E)qv[i + t];
+    }
+    float dqa[DQ];
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) dqa[i] = 0.f;
+    int rb = 0, pj = kB;  // local row base of band depth j, b^(j+1)
+    for (int j = 0; j < nb; ++j, rb += pj, pj *= kB) {
+      const int d = da + j, sh = lb * (T - d);
+      const int n = leaf >> sh;
+      const bool rep = valid && (u == 0 || (sl[u - 1] >> sh) != n);
+      // the node's child logits (every lane takes part in the reductions)
+      const float* cr = sum + ((int64_t)G.off[d + 1] + kB * n) * D + tq * DQ;
+      float x[kB];
+#pragma unroll
+      for (int c = 0; c < kB; ++c) {
+        if (c > 0 && a.pair_rows) {
+          x[c] = -x[0];
+          continue;
+        }
+        float p = 0.f;
+#pragma unroll
+        for (int i = 0; i < DQ; i += 4) {
+          const float4 cv = *(const float4*)(cr + (int64_t)c * D + i);
+          p += qv[i] * cv.x + qv[i + 1] * cv.y + qv[i + 2] * cv.z + qv[i + 3] * cv.w;
+        }
+        p += __shfl_xor(p, 1, 64);
+        p += __shfl_xor(p, 2, 64);
+        x[c] = p;
+      }
+      if (!rep) continue;
+      float An = 0.f, Ac[kB];
+#pragma unroll
+      for (int c = 0; c < kB; ++c) Ac[c] = 0.f;
+      for (int v2 = u; v2 < cnt; ++v2) {
+        const int lf2 = sl[v2];
+        if ((lf2 >> sh) != n) break;
+        const float dv = dls[v2];
+        const int dig = (lf2 >> (sh - lb)) & (kB - 1);
+        An += dv;
+#pragma unroll
+        for (int c = 0; c < kB; ++c)
+          if (c == dig) Ac[c] += dv;
+      }
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < kB; ++c) mx = fmaxf(mx, clamp_h(x[c], a.maxhalf));
+      float ex[kB], se = 0.f;
+#pragma unroll
+      for (int c = 0; c < kB; ++c) {
+        ex[c] = __expf(clamp_h(x[c], a.maxhalf) - mx);
+        se += ex[c];
+      }
+      float gc[kB];
+#pragma unroll
+      for (int c = 0; c < kB; ++c) {
+        const bool live = x[c] >= -a.maxhalf && x[c] <= a.maxhalf;
+        gc[c] = live ? Ac[c] - ex[c] / se * An : 0.f;
+      }
+      if (a.pair_rows) {
+        const float gd = gc[0] - gc[1];  // c_right = -c_left
+#pragma unroll
+        for (int i = 0; i < DQ; i += 4) {
+          const float4 cv = *(const float4*)(cr + i);
+          dqa[i] += gd * cv.x; dqa[i + 1] += gd * cv.y; dqa[i + 2] += gd * cv.z; dqa[i + 3] += gd * cv.w;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < kB; ++c)
+#pragma unroll
+          for (int i = 0; i < DQ; i += 4) {
+            const float4 cv = *(const float4*)(cr + (int64_t)c * D + i);
+            dqa[i] += gc[c] * cv.x; dqa[i + 1] += gc[c] * cv.y; dqa[i + 2] += gc[c] * cv.z; dqa[i + 3] += gc[c] * cv.w;
+          }
+      }
+      if (tq == 0) {
+        const int r0 = rb + kB * (n - (s0 << (lb * j)));
+#pragma unroll
+        for (int c = 0; c < kB; ++c) Gt[(r0 + c) * GS + tp] = (E)gc[c];
+      }
+    }
+    if (valid) {
+      E* dr = (E*)a.dq_part + (qh * S + u) * D + tq * DQ;
+#pragma unroll
+      for (int i = 0; i < DQ; i += 8) {
+        float o[8];
+        if (a.rmw) ld8f(o, dr + i);
+        else
+#pragma unroll
+          for (int t = 0; t < 8; ++t) o[t] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] += dqa[i + t];
+        if constexpr (sizeof(E) == 2) {
+          typedef __attribute__((ext_vector_type(8))) E e8;
+          e8 v;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = (E)o[t];
+          *(e8*)(dr + i) = v;
+        } else {
+          *(float4*)(dr + i) = make_float4(o[0], o[1], o[2], o[3]);
+          *(float4*)(dr + i + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+      }
+    }
+    __syncthreads();
+    // dC_sub (band rows x D) += G_tile (rows x 64 pairs) Q_tile (64 pairs x D)
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+      const int t = w + 4 * k;
+      if (t >= ntu) continue;
+      const int rt = t / NCT, ct = t - rt * NCT;
+#pragma unroll
+      for (int ks = 0; ks < 64 / M::K; ++ks) {
+        const F af = ld_frag(Gt + (16 * rt + col) * GS + ks * M::K + M::KPL * g);
+        F bf;
+        if constexpr (M::KPL == 1) bf = Qs[(ks * M::K + g) * QS + 16 * ct + col];
+        else bf = tr_frag<E>(Qs, QS, ks * M::K + 8 * g, ks * M::K + 8 * g + 4, 16 * ct, lane);
+        acc[k] = M::mma(af, bf, acc[k]);
+      }
+    }
+    __syncthreads();
+  }
+  // the subtree's band rows of dC: local row rb_j + r -> level da + j + 1, row s0 b^(j+1) + r
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    const int t = w + 4 * k;
+    if (t >= ntu) continue;
+    const int rt = t / NCT, ct = t - rt * NCT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int lr = 16 * rt + 4 * g + r;
+      if (lr >= R) continue;
+      int j = 0, pj = kB;
+      while (lr >= pj) {
+        lr -= pj;
+        pj *= kB;
+        ++j;
+      }
+      const int64_t grow = G.off[da + j + 1] + ((int64_t)s0 << (lb * (j + 1))) + lr;
+      a.dsum[((int64_t)bh * G.NS + grow) * D + 16 * ct + col] = acc[k][r];
+    }
+  }
+}
+
+// Reference causal mode at the band depths: the boundary children's part of
+// dC, dC[left child of n] += sum_t g_t q_t and dC[right child] -= the same,
+// over the queries t whose boundary node at depth d is n (t >> (T - d) = n, a
+// contiguous range; rc_g from ref_causal_grad_kernel).  One thread per (node,
+// eight head dims), queries in order; runs after the band kernels wrote these
+// rows.  grid (ceil(2^d D / 8 / 256), B*H).
+template <typename E>
+__global__ __launch_bounds__(256) void ref_band_boundary_kernel(TreeArgs a, int d) {
+  const Geo& G = a.geo;
+  const int D = a.D, T = G.T;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= ((int64_t)1 << d) * (D / 8)) return;
+  const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
+  const int n = (int)(e / (D / 8)), d0 = (int)(e - (int64_t)n * (D / 8)) * 8;
+  const int t_lo = max(n << (T - d), a.t0), t_hi = min((n + 1) << (T - d), a.L);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  bool any = false;
+  for (int t = t_lo; t < t_hi; ++t) {
+    const float gv = a.rc_g[(((int64_t)bb * a.L + t) * a.H + h) * T + d];
+    if (gv == 0.f) continue;
+    any = true;
+    float qv[8];
+    ld8f(qv, (const E*)a.q + bb * a.qsb + (int64_t)t * a.qsl + h * a.qsh + d0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += gv * qv[i];
+  }
+  if (!any) return;
+  float* left = a.dsum + ((int64_t)bh * G.NS + G.off[d + 1] + 2 * n) * D + d0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    left[i] += acc[i];
+    left[D + i] -= acc[i];
+  }
 }
 
 static int tree_smem(const Plan& P) {
@@ -1010,6 +1319,11 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.dstar = (const int*)(rec + P.rec.dstar);
   a.rc_coef = (float*)(ws + P.bws.rc_coef);
   a.rc_rho = (float*)(ws + P.bws.rc_rho);
+  a.rc_g = (float*)(ws + P.bws.rc_g);
+  a.Tb = P.tree_dense;
+  a.nsd = P.geo.off[P.tree_dense + 1];
+  a.dqp = P.geo.LB > 1 || P.tree_dense < P.geo.T;
+  a.dkl = P.geo.LB > 1 && P.p.tree_mode != TA_TREE_NODEKEYS;
 
   const int64_t nqh = P.B * P.L * P.H;
   int pw2 = 1;
@@ -1018,6 +1332,37 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
                      a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh);
   if (a.refc)
     hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
+  // the band depths (before tree_dq_kernel, whose epilogue sums the pairs' dq rows)
+  if (P.tree_dense < P.geo.T) {
+    const int b = P.geo.b, nbmax = b == 2 ? 5 : 2;
+    BandArgs ba;
+    ba.geo = P.geo;
+    ba.L = (int)P.L;
+    ba.H = (int)P.H;
+    ba.S = (int)P.S;
+    ba.pair_rows = P.p.tree_mode != TA_TREE_NATURAL && b == 2;
+    ba.maxhalf = a.maxhalf;
+    ba.q = q;
+    ba.qsb = a.qsb; ba.qsl = a.qsl; ba.qsh = a.qsh;
+    ba.sum32 = (const float*)(rec + P.rec.summaries);
+    ba.slot_leaf = a.slot_leaf;
+    ba.slot_count = a.slot_count;
+    ba.dl = a.dl;
+    ba.order = (const int*)(rec + P.rec.order);
+    ba.block_start = (const int*)(rec + P.rec.block_start);
+    ba.dq_part = ws + P.bws.dq_part;
+    ba.dsum = a.dsum;
+    for (int da = P.tree_dense; da < P.geo.T; da += nbmax) {
+      ba.da = da;
+      ba.nb = P.geo.T - da < nbmax ? P.geo.T - da : nbmax;
+      ba.R = 0;
+      for (int j = 0, pj = b; j < ba.nb; ++j, pj *= b) ba.R += pj;
+      ba.rmw = P.geo.LB > 1 || da > P.tree_dense;  // leaf dq rows exist, or an earlier band wrote them
+      const dim3 grid((unsigned)P.geo.pw[da], (unsigned)P.BH);
+      if (b == 2) hipLaunchKernelGGL((tree_band_kernel<E, D, 2>), grid, dim3(256), 0, st, ba);
+      else hipLaunchKernelGGL((tree_band_kernel<E, D, 4>), grid, dim3(256), 0, st, ba);
+    }
+  }
   const int smem_q = tree_smem(P);
   const unsigned qtiles = (unsigned)(P.Lp / kQueryTile);
   auto launch_dq = [&](auto kern) -> hipError_t {
@@ -1034,12 +1379,18 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   else if (P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 16, 2>);
   else e = launch_dq(tree_dq_kernel<E, D, 16, 0>);
   if (e != hipSuccess) return e;
-  if (P.geo.T > 0) {
-    const unsigned chunks = (unsigned)((P.geo.NS / 16 + 8 * kDcRows - 1) / (8 * kDcRows));
+  if (a.refc)
+    for (int d = P.tree_dense; d < P.geo.T; ++d) {
+      const int64_t n = ((int64_t)1 << d) * (D / 8);
+      hipLaunchKernelGGL(ref_band_boundary_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a,
+                         d);
+    }
+  if (a.nsd > 0) {
+    const unsigned chunks = (unsigned)((a.nsd / 16 + 8 * kDcRows - 1) / (8 * kDcRows));
     hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(chunks, P.qsplit, P.BH), dim3(512), 0, st, a);
-    const int64_t n = P.BH * (int64_t)P.geo.NS * D;
+    const int64_t n = P.BH * (int64_t)a.nsd * D;
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D);
+                       (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D, a.nsd);
   }
   if (P.p.tree_mode == TA_TREE_NODEKEYS) {
     const int64_t n = (int64_t)(P.geo.NL - 1) * D;

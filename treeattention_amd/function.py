@@ -54,6 +54,10 @@ class TreeOptions:
     * ``seed``: counter-RNG key for the Gumbel uniforms when no explicit
       ``uniforms`` tensor is given.
     * ``layout``: ``"bshd"`` (B, L, H, D) or ``"lbhd"`` (L, B, H, D).
+    * ``dense_cols``: tree levels with at most this many children are
+      evaluated as dense level tiles, wider ones per sampled path (0: the
+      library's defaults); for tuning and tests, results change only by
+      rounding.
     """
 
     num_samples: int
@@ -66,6 +70,7 @@ class TreeOptions:
     max_logit: float = 1e3
     seed: int = 0
     layout: str = "bshd"
+    dense_cols: int = 0
 
 
 def _bl(t: torch.Tensor, layout: str) -> tuple[int, int]:
@@ -127,6 +132,7 @@ def make_problem(q, k, v, opts: TreeOptions) -> _lib.Problem:
     p.dtype = _DTYPES[q.dtype]
     p.scale = float(opts.scale) if opts.scale is not None else 1.0 / math.sqrt(D)
     p.max_logit = float(opts.max_logit)
+    p.dense_cols = int(opts.dense_cols)
     p.q_strides[:] = _strides(q, opts.layout)
     p.k_strides[:] = _strides(k, opts.layout)
     p.v_strides[:] = _strides(v, opts.layout)
