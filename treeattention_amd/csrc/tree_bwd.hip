@@ -1002,7 +1002,8 @@ __global__ __launch_bounds__(256) void nodekeys_adjoint_kernel(TreeArgs a) {
 // band's work under node s of depth da is one workgroup: the subtree's
 // (query, distinct leaf block) pairs are one contiguous run of the bucket
 // order (pairs sorted by leaf block are sorted by node at every depth), taken
-// 64 at a time, four threads per pair.  At depth d of the band the query's
+// 32 at a time, eight threads per pair (the query's distinct leaf blocks staged
+// in LDS).  At depth d of the band the query's
 // slots under the pair's node n form a run, and its first slot (the run's
 // representative) carries the node's entries of G:
 //   G[n, j] = A_j - p_j A_n
@@ -1046,22 +1047,26 @@ __device__ __forceinline__ void ld8f(float* o, const E* p) {
 }
 
 template <typename E, int D, int kB>
-__global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
+__global__ __launch_bounds__(256, 2) void tree_band_kernel(BandArgs a) {
   using M = Mfma<E>;
   using F = typename M::frag;
-  constexpr int DQ = D / 4;  // head dims per thread
+  constexpr int TPP = 8;           // threads per pair
+  constexpr int PC = 256 / TPP;    // pairs per chunk (the MFMA k of the dC product)
+  constexpr int DQ = D / TPP;      // head dims per thread: 4, 8, 12 or 16
   constexpr int lb = kB == 2 ? 1 : 2;
-  constexpr int GS = 64 + (sizeof(E) == 2 ? 8 : 4);  // G tile row stride (elements)
+  constexpr int GS = PC + (sizeof(E) == 2 ? 8 : 4);  // G tile row stride (elements)
   constexpr int QS = D + (sizeof(E) == 2 ? 8 : 4);   // Q tile row stride
   constexpr int NCT = D / 16;
   constexpr int NT = (kBandRows / 16) * NCT;  // output tiles at most
   constexpr int TPW = (NT + 3) / 4;
   __shared__ __align__(16) E Gt[kBandRows * GS];  // [band row][pair]
-  __shared__ __align__(16) E Qs[64 * QS];         // [pair][dim]
+  __shared__ __align__(16) E Qs[PC * QS];         // [pair][dim]
+  __shared__ int Sl[PC * kMaxSamples];            // each pair's query: its distinct leaf blocks
+  __shared__ float Sd[PC * kMaxSamples];          //   and their dl
   const Geo& G = a.geo;
   const int s0 = blockIdx.x, bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
-  const int tp = tid >> 2, tq = tid & 3;
+  const int tp = tid / TPP, tq = tid % TPP;
   const int T = G.T, S = a.S, da = a.da, nb = a.nb, R = a.R;
   const int RP = (R + 15) & ~15, ntu = (RP / 16) * NCT;
   const int span = 1 << (lb * (T - da));  // leaf blocks under the subtree
@@ -1069,32 +1074,42 @@ __global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
   const int e_begin = bs[s0 * span], e_end = bs[(s0 + 1) * span];
   const int* ord = a.order + (int64_t)bh * a.L * S;
   const float* sum = a.sum32 + (int64_t)bh * G.NS * D;
+  int* sl = Sl + tp * kMaxSamples;
+  float* sd = Sd + tp * kMaxSamples;
 
   f32x4 acc[TPW];
 #pragma unroll
   for (int k = 0; k < TPW; ++k) acc[k] = zero4();
-  for (int e0 = e_begin; e0 < e_end; e0 += 64) {
-    for (int e = tid; e < RP * 64; e += 256) Gt[(e >> 6) * GS + (e & 63)] = (E)0.f;
+  for (int e0 = e_begin; e0 < e_end; e0 += PC) {
+    for (int e = tid; e < RP * PC; e += 256) Gt[(e / PC) * GS + (e % PC)] = (E)0.f;
     const int e = e0 + tp;
     const bool valid = e < e_end;
     const int ent = valid ? ord[e] : 0;
     const int l = ent / S, u = ent - l * S;
     const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
-    const int* sl = a.slot_leaf + qh * S;
-    const float* dls = a.dl + qh * S;
     const int cnt = valid ? a.slot_count[qh] : 0;
-    const int leaf = valid ? sl[u] : 0;
+    for (int v = tq; v < cnt; v += TPP) {
+      sl[v] = a.slot_leaf[qh * S + v];
+      sd[v] = a.dl[qh * S + v];
+    }
     float qv[DQ];
     const E* qr = (const E*)a.q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + tq * DQ;
 #pragma unroll
-    for (int i = 0; i < DQ; i += 8) {
-      if (valid) ld8f(qv + i, qr + i);
-      else
+    for (int i = 0; i < DQ; i += 4) {
+      if constexpr (sizeof(E) == 2) {
+        typedef __attribute__((ext_vector_type(4))) E e4;
+        const e4 x = valid ? *(const e4*)(qr + i) : e4{(E)0.f, (E)0.f, (E)0.f, (E)0.f};
 #pragma unroll
-        for (int t = 0; t < 8; ++t) qv[i + t] = 0.f;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) Qs[tp * QS + tq * DQ + i + t] = (E)qv[i + t];
+        for (int t = 0; t < 4; ++t) qv[i + t] = (float)x[t];
+        *(e4*)(Qs + tp * QS + tq * DQ + i) = x;
+      } else {
+        const float4 x = valid ? *(const float4*)(qr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qv[i] = x.x; qv[i + 1] = x.y; qv[i + 2] = x.z; qv[i + 3] = x.w;
+        *(float4*)(Qs + tp * QS + tq * DQ + i) = x;
+      }
     }
+    __syncthreads();  // the pairs' slot lists
+    const int leaf = valid ? sl[u] : 0;
     float dqa[DQ];
 #pragma unroll
     for (int i = 0; i < DQ; ++i) dqa[i] = 0.f;
@@ -1120,6 +1135,7 @@ __global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
         }
         p += __shfl_xor(p, 1, 64);
         p += __shfl_xor(p, 2, 64);
+        p += __shfl_xor(p, 4, 64);
         x[c] = p;
       }
       if (!rep) continue;
@@ -1129,7 +1145,7 @@ __global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
       for (int v2 = u; v2 < cnt; ++v2) {
         const int lf2 = sl[v2];
         if ((lf2 >> sh) != n) break;
-        const float dv = dls[v2];
+        const float dv = sd[v2];
         const int dig = (lf2 >> (sh - lb)) & (kB - 1);
         An += dv;
 #pragma unroll
@@ -1176,35 +1192,37 @@ __global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
     if (valid) {
       E* dr = (E*)a.dq_part + (qh * S + u) * D + tq * DQ;
 #pragma unroll
-      for (int i = 0; i < DQ; i += 8) {
-        float o[8];
-        if (a.rmw) ld8f(o, dr + i);
-        else
-#pragma unroll
-          for (int t = 0; t < 8; ++t) o[t] = 0.f;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[t] += dqa[i + t];
+      for (int i = 0; i < DQ; i += 4) {
+        float o[4] = {dqa[i], dqa[i + 1], dqa[i + 2], dqa[i + 3]};
         if constexpr (sizeof(E) == 2) {
-          typedef __attribute__((ext_vector_type(8))) E e8;
-          e8 v;
+          typedef __attribute__((ext_vector_type(4))) E e4;
+          if (a.rmw) {
+            const e4 y = *(const e4*)(dr + i);
 #pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] = (E)o[t];
-          *(e8*)(dr + i) = v;
+            for (int t = 0; t < 4; ++t) o[t] += (float)y[t];
+          }
+          e4 v;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = (E)o[t];
+          *(e4*)(dr + i) = v;
         } else {
+          if (a.rmw) {
+            const float4 y = *(const float4*)(dr + i);
+            o[0] += y.x; o[1] += y.y; o[2] += y.z; o[3] += y.w;
+          }
           *(float4*)(dr + i) = make_float4(o[0], o[1], o[2], o[3]);
-          *(float4*)(dr + i + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
       }
     }
-    __syncthreads();
-    // dC_sub (band rows x D) += G_tile (rows x 64 pairs) Q_tile (64 pairs x D)
+    __syncthreads();  // the G tile
+    // dC_sub (band rows x D) += G_tile (rows x PC pairs) Q_tile (PC pairs x D)
 #pragma unroll
     for (int k = 0; k < TPW; ++k) {
       const int t = w + 4 * k;
       if (t >= ntu) continue;
       const int rt = t / NCT, ct = t - rt * NCT;
 #pragma unroll
-      for (int ks = 0; ks < 64 / M::K; ++ks) {
+      for (int ks = 0; ks < PC / M::K; ++ks) {
         const F af = ld_frag(Gt + (16 * rt + col) * GS + ks * M::K + M::KPL * g);
         F bf;
         if constexpr (M::KPL == 1) bf = Qs[(ks * M::K + g) * QS + 16 * ct + col];
@@ -1212,7 +1230,7 @@ __global__ __launch_bounds__(256) void tree_band_kernel(BandArgs a) {
         acc[k] = M::mma(af, bf, acc[k]);
       }
     }
-    __syncthreads();
+    __syncthreads();  // G tile, Q tile and slot lists are rewritten next chunk
   }
   // the subtree's band rows of dC: local row rb_j + r -> level da + j + 1, row s0 b^(j+1) + r
 #pragma unroll
