@@ -217,9 +217,18 @@ def test_odd_leaf_blocks_and_partial_query_tiles(b, LB, L, D, causal, dtype):
 
 
 def test_large_bucket_histogram():
-    # 4096 leaf blocks x 64 query chunks: the bucket counts are scanned in
-    # segments by several workgroups per (batch, head)
-    run_case(1, 16384, 1, 32, 4, 4, 4, "natural", False, torch.bfloat16)
+    # 2048 leaf blocks (one counting-sort window) x 64 query chunks: the bucket
+    # counts are scanned in segments by several workgroups per (batch, head)
+    run_case(1, 16384, 1, 32, 4, 2, 8, "natural", False, torch.bfloat16)
+
+
+@pytest.mark.parametrize("B,H,L,b,LB,S,causal", [(1, 1, 16384, 4, 4, 4, False), (2, 2, 8192, 2, 2, 8, True),
+                                                (2, 8, 4096, 2, 1, 4, False)])
+def test_bucketing_by_radix_sort(B, H, L, b, LB, S, causal):
+    # more than 2048 leaf blocks: pairs are bucketed by a stable radix sort of
+    # (batch * head, leaf block) keys (two or three 8-bit passes here), whose order
+    # must equal the counting sort's (query order within a block)
+    run_case(B, L, H, 32, S, b, LB, "natural", causal, torch.bfloat16, dense_cols=64 if LB == 1 else 0)
 
 
 @pytest.mark.parametrize("causal", [False, True])

@@ -13,7 +13,7 @@
 
 namespace ta {
 
-constexpr int kWin = 2048;                 // leaf blocks per LDS window
+constexpr int kWin = kBucketWin;           // leaf blocks per LDS window
 constexpr int kWords = kQueryChunk / 32;  // bitmask words per block
 
 struct BucketArgs {
@@ -241,6 +241,165 @@ __global__ __launch_bounds__(1024) void bucket_pieces_kernel(BucketArgs a) {
   bucket_pieces(a, bh, a.block_start + (int64_t)bh * (a.NL + 1), part, threadIdx.x);
 }
 
+// Many leaf blocks (more than one LDS window, e.g. the reference's one-token
+// leaves): the (block x query chunk) table would grow as NL L; instead every
+// slot becomes a key (batch * head) * (NL + 1) + leaf block (NL for the slots
+// past a query's count) with value l * S + u, in (batch, position, head, slot)
+// order, and a stable LSD radix sort orders them: within one (batch, head) and
+// leaf block the values keep their (l, u) order -- exactly the counting sort's
+// result -- and each (batch, head)'s L S entries, its pairs first, land in its
+// own range of `order`.  The block starts are an exclusive scan of per-block
+// counts.  Per 8-bit digit: per-tile digit counts, exclusive scans of the
+// per-digit rows over tiles, then a scatter whose ranks within a tile come from wavefront
+// ballots (peers with the same digit) and per-wave digit counts in LDS.  No
+// atomics decide any order; no memset or library call (graph-capture safe).
+constexpr int kSortTile = 2048;  // elements per workgroup: 8 rounds of 256
+
+__global__ __launch_bounds__(256) void sort_keys_kernel(BucketArgs a, uint32_t* keys, int* vals, int* cnt,
+                                                        int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t qh = i / a.S;
+  const int u = (int)(i - qh * a.S);
+  const int h = (int)(qh % a.H);
+  const int64_t bl = qh / a.H;
+  const int l = (int)(bl % a.L), bb = (int)(bl / a.L);
+  const int64_t bh = (int64_t)bb * a.H + h;
+  const bool act = u < a.slot_count[qh];
+  const int leaf = act ? a.slot_leaf[i] : a.NL;
+  keys[i] = (uint32_t)(bh * (a.NL + 1) + leaf);
+  vals[i] = l * a.S + u;
+  if (act) atomicAdd(cnt + bh * a.NL + leaf, 1);  // counts: order-free
+}
+
+__global__ __launch_bounds__(256) void zero_ints_kernel(int* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// th[digit * ntiles + tile] = elements of the tile with that digit
+__global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                                                         int* __restrict__ th, int ntiles) {
+  __shared__ int cnt[256];
+  const int tile = blockIdx.x, tid = threadIdx.x;
+  cnt[tid] = 0;
+  __syncthreads();
+  for (int r = 0; r < kSortTile / 256; ++r) {
+    const int64_t i = (int64_t)tile * kSortTile + r * 256 + tid;
+    if (i < n) atomicAdd(&cnt[(keys[i] >> shift) & 255], 1);
+  }
+  __syncthreads();
+  th[(int64_t)tid * ntiles + tile] = cnt[tid];
+}
+
+// exclusive scan of each digit's row th[digit, :] in place (one workgroup of
+// 1024 threads per digit), the row's total into dtot[digit]
+__global__ __launch_bounds__(1024) void radix_scan_kernel(int* th, int ntiles, int* dtot) {
+  __shared__ int part[16];
+  const int tid = threadIdx.x;
+  int* row = th + (int64_t)blockIdx.x * ntiles;
+  const int per = (ntiles + 1023) / 1024, s0 = min(ntiles, tid * per), s1 = min(ntiles, s0 + per);
+  int sum = 0;
+  for (int i = s0; i < s1; ++i) sum += row[i];
+  int total;
+  int run = block_scan_1024(sum, part, tid, total);
+  for (int i = s0; i < s1; ++i) {
+    const int x = row[i];
+    row[i] = run;
+    run += x;
+  }
+  if (tid == 0) dtot[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(256) void radix_scatter_kernel(const uint32_t* __restrict__ kin,
+                                                            const int* __restrict__ vin, uint32_t* __restrict__ kout,
+                                                            int* __restrict__ vout, int64_t n, int shift,
+                                                            const int* __restrict__ th, int ntiles,
+                                                            const int* __restrict__ dtot) {
+  __shared__ int base[256];
+  __shared__ int wcnt[4][256];
+  const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // digit tid's first output: the counts of all smaller digits plus this
+  // digit's count in earlier tiles
+  {
+    const int t = dtot[tid];
+    int x = t;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wcnt[0][w] = x;
+    __syncthreads();
+    int pre = x - t;
+    for (int k = 0; k < w; ++k) pre += wcnt[0][k];
+    base[tid] = pre + th[(int64_t)tid * ntiles + tile];
+    __syncthreads();
+  }
+  const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+  for (int r = 0; r < kSortTile / 256; ++r) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wcnt[k][tid] = 0;
+    __syncthreads();
+    const int64_t i = (int64_t)tile * kSortTile + r * 256 + tid;
+    const bool in = i < n;
+    const uint32_t key = in ? kin[i] : 0u;
+    const int val = in ? vin[i] : 0;
+    const int dg = (int)((key >> shift) & 255);
+    uint64_t peers = __ballot(in);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t bb = __ballot((dg >> bit) & 1);
+      peers &= ((dg >> bit) & 1) ? bb : ~bb;
+    }
+    const int below = __popcll(peers & lt);
+    if (in && below == 0) wcnt[w][dg] = __popcll(peers);
+    __syncthreads();
+    if (in) {
+      int64_t pos = (int64_t)(unsigned)base[dg] + below;
+      for (int k = 0; k < w; ++k) pos += wcnt[k][dg];
+      kout[pos] = key;
+      vout[pos] = val;
+    }
+    __syncthreads();
+    base[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+  }
+}
+
+static int sort_key_bits(const Plan& P) {
+  int bits = 1;
+  while (bits < 32 && ((int64_t)1 << bits) < P.BH * (P.geo.NL + 1)) ++bits;
+  return bits;
+}
+
+static hipError_t bucket_by_sort(const Plan& P, BucketArgs& a, char* rec, hipStream_t st) {
+  const int64_t n = P.B * P.L * P.H * P.S;
+  uint32_t* k0 = (uint32_t*)(rec + P.rec.sort_keys);
+  uint32_t* k1 = k0 + n;
+  int* v0 = (int*)(rec + P.rec.sort_vals);
+  int* v1 = v0 + n;
+  int* th = (int*)(rec + P.rec.sort_hist);
+  const int ntiles = (int)((n + kSortTile - 1) / kSortTile);
+  int* dtot = th + (int64_t)256 * ntiles;  // per-digit totals of a pass
+  const int64_t ncnt = P.BH * P.geo.NL;
+  hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((ncnt + 255) / 256)), dim3(256), 0, st, a.hist, ncnt);
+  hipLaunchKernelGGL(sort_keys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, k0, v0, a.hist, n);
+  const int bits = sort_key_bits(P), npass = (bits + 7) / 8;
+  for (int ps = 0; ps < npass; ++ps) {
+    const int shift = 8 * ps;
+    // values ping-pong v0 -> v1 -> v0 ..., the last pass writes `order`
+    const uint32_t* kin = ps & 1 ? k1 : k0;
+    uint32_t* kout = ps & 1 ? k0 : k1;
+    const int* vin = ps & 1 ? v1 : v0;
+    int* vout = ps + 1 == npass ? a.order : (ps & 1 ? v0 : v1);
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(ntiles), dim3(256), 0, st, kin, n, shift, th, ntiles);
+    hipLaunchKernelGGL(radix_scan_kernel, dim3(256), dim3(1024), 0, st, th, ntiles, dtot);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3(ntiles), dim3(256), 0, st, kin, vin, kout, vout, n, shift, th,
+                       ntiles, dtot);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
   BucketArgs a;
   a.L = (int)P.L;
@@ -258,6 +417,19 @@ hipError_t launch_bucket(const Plan& P, char* rec, hipStream_t st) {
   a.piece_block = (int*)(rec + P.rec.piece_block);
   a.nseg = P.nseg;
   a.seg_sum = (int*)(rec + P.rec.seg_sum);
+  if (P.bucket_sort) {
+    hipError_t e = bucket_by_sort(P, a, rec, st);
+    if (e != hipSuccess) return e;
+    // nchunk is 1: the scan turns the counts into block starts and pieces
+    if (P.nseg > 4) {
+      hipLaunchKernelGGL(bucket_segsum_kernel, dim3(P.nseg, P.BH), dim3(1024), 0, st, a);
+      hipLaunchKernelGGL(bucket_segscan_kernel, dim3(P.nseg, P.BH), dim3(1024), 0, st, a);
+      hipLaunchKernelGGL(bucket_pieces_kernel, dim3(P.BH), dim3(1024), 0, st, a);
+    } else {
+      hipLaunchKernelGGL(bucket_scan_kernel, dim3(P.BH), dim3(1024), 0, st, a);
+    }
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(bucket_pass_kernel<false>, dim3(P.nchunk, P.BH), dim3(kQueryChunk), 0, st, a);
   if (P.nseg > 4) {
     hipLaunchKernelGGL(bucket_segsum_kernel, dim3(P.nseg, P.BH), dim3(1024), 0, st, a);

@@ -133,9 +133,17 @@ int make_plan(const ta_problem* p, Plan* P) {
       }
   const int64_t NSd = G.off[P->tree_dense + 1];  // dense rows
 
-  // bucketing: one count per (leaf block, chunk of kQueryChunk queries)
+  // bucketing: one count per (leaf block, chunk of kQueryChunk queries), or
+  // with more leaf blocks than one LDS window a radix sort and one count per block
   P->qc = kQueryChunk;
-  P->nchunk = (int)((L + kQueryChunk - 1) / kQueryChunk);
+  P->bucket_sort = NL > kBucketWin;
+  P->nchunk = P->bucket_sort ? 1 : (int)((L + kQueryChunk - 1) / kQueryChunk);
+  if (P->bucket_sort && B * H * (NL + 1) > ((int64_t)1 << 32) - 1)
+    return fail(TA_ERR_UNSUPPORTED, "B*H*(N/leaf_block + 1) must be < 2^32 (got %lld)",
+                (long long)(B * H * (NL + 1)));
+  if (B * L * H * S >= ((int64_t)1 << 32)) return fail(TA_ERR_UNSUPPORTED, "B*L*H*num_samples must be < 2^32");
+  if (P->bucket_sort && B * L * H * S >= ((int64_t)1 << 31))
+    return fail(TA_ERR_UNSUPPORTED, "with more than %d leaf blocks B*L*H*num_samples must be < 2^31", kBucketWin);
   P->npiece = (int)(NL + (L * S + kPieceFwd - 1) / kPieceFwd);
   if ((int64_t)P->npiece * P->BH > ((int64_t)1 << 31) - 1)
     return fail(TA_ERR_UNSUPPORTED, "too many leaf-forward pieces (NL=%lld)", (long long)NL);
@@ -176,6 +184,10 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.seg_sum = r.take(P->BH * P->nseg * 4);
   P->rec.dstar = r.take(p->causal == TA_CAUSAL_REFERENCE ? L * 4 : 0);
   P->rec.logA = r.take(p->causal == TA_CAUSAL_EXACT && P->sample_dense < T ? B * L * H * (T + 1) * 4 : 0);
+  // the radix sort's key and value double buffers and per-tile digit counts
+  P->rec.sort_keys = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
+  P->rec.sort_vals = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
+  P->rec.sort_hist = r.take(P->bucket_sort ? 256 * ((BLHS + 2047) / 2048 + 1) * 4 : 0);
   P->rec.total = r.at;
   const bool lb1 = LB == 1;  // leaf stage: a value gather, no pair rows
   Carver f;

@@ -524,6 +524,9 @@ struct RecordLayout {
   int64_t seg_sum;     // int (BH, nseg): bucket counts per histogram scan segment
   int64_t dstar;       // int (L): reference causal mode: first uncorrected depth per query
   int64_t logA;        // float (B, L, H, T + 1): exact causal with sparse levels, boundary log-masses
+  int64_t sort_keys;   // uint32 (2, B, L, H, S): bucketing by sort, key double buffer
+  int64_t sort_vals;   // int (2, B, L, H, S): bucketing by sort, value double buffer
+  int64_t sort_hist;   // int (256, tiles of 2048 keys + 1): the sort's per-tile digit counts, digit totals
   int64_t total;
 };
 
@@ -548,6 +551,7 @@ struct BwdWorkspaceLayout {
 };
 
 constexpr int kQueryChunk = 256; // queries per bucketing chunk (one wavefront each)
+constexpr int kBucketWin = 2048; // leaf blocks the counting sort's LDS window holds; more sort by keys
 // A leaf block's pairs are cut into pieces of at most kPieceFwd pairs, one
 // leaf-forward workgroup each, so the heavy low blocks of causal runs (a
 // block near the start is reachable from every later query) do not leave

@@ -19,6 +19,7 @@ struct Plan {
   int qsplit;       // query splits of the summary-gradient product
   int sample_dense; // the sampler's level tiles cover depths < sample_dense; deeper levels are sparse
   int tree_dense;   // the backward's dense G tiles cover depths < tree_dense; deeper ones run in bands
+  int bucket_sort;  // many leaf blocks: bucketing by a radix sort of (batch * head, leaf block) keys
   RecordLayout rec;
   FwdWorkspaceLayout fws;
   BwdWorkspaceLayout bws;
