@@ -99,14 +99,20 @@ def tree_units(B, L, H, D, e, b, LB, S):
     )
 
 
-def read_traffic(phase: str, config: str):
-    """HBM bytes per launch of `phase`'s main kernel from the committed rocprofv3 counter summary
-    (``profiles/traffic_<config>.md``, FETCH_SIZE/WRITE_SIZE calibrated by a plain copy), or None."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{config}.md")
+def read_profile(kind: str, key: str, phase: str, config: str):
+    """A figure of `phase`'s main kernel from a committed rocprofv3 counter summary
+    ``profiles/<kind>_<config>.md`` (a line ``key[phase]: value``), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{config}.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_launch\[" + re.escape(phase) + r"\]:\s*([0-9.eE+]+)", open(path).read())
+    m = re.search(re.escape(key) + r"\[" + re.escape(phase) + r"\]:\s*([0-9.eE+]+)", open(path).read())
     return float(m.group(1)) if m else None
+
+
+def read_traffic(phase: str, config: str):
+    """HBM bytes per launch of `phase`'s main kernel (``profiles/traffic_<config>.md``: FETCH_SIZE and
+    WRITE_SIZE calibrated by a plain copy), or None."""
+    return read_profile("traffic", "traffic_bytes_per_launch", phase, config)
 
 
 # Queries timed per config by the CPU baseline (all heads of batch element 0, the
@@ -391,6 +397,11 @@ def main() -> int:
         achieved, peak, unit = units / t_s / 1e9, HBM_PEAK_GBS, "GB/s"
     roofline = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": read_traffic(dom, args.config), "kernel": dom}
+    if bound == "mfma":
+        # the same fraction by counters (profiles/mfma_<config>.md): issued MFMA flops / duration / peak,
+        # and the matrix cores' busy share of SIMD-cycles
+        roofline["frac_counter"] = read_profile("mfma", "mfma_counter_frac", dom, args.config)
+        roofline["mfma_util_pct_counter"] = read_profile("mfma", "mfma_util_pct", dom, args.config)
     per_phase = {}
     for name, (bd, un) in kern.items():
         ts = phase_ms[name] / 1e3

@@ -190,3 +190,29 @@ def test_reference_tree_buffers_linear_in_length(causal):
     assert sizes[65536][2] < 24 * 2**30  # fits one GPU with room (was 565 GB)
     assert sizes[65536][0] < 4.4 * sizes[16384][0]
     assert sizes[65536][0] < 8 * 2**30
+
+
+def test_bench_reads_committed_counter_summaries():
+    """bench.py's roofline object takes its traffic and counter MFMA figures from the committed
+    rocprofv3 summaries; every summary present must parse and hold plausible values."""
+    import importlib.util
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    found = 0
+    for cfg in bench.CONFIGS:
+        if os.path.exists(os.path.join(root, "profiles", f"traffic_{cfg}.md")):
+            t = bench.read_traffic("leaf_backward", cfg)
+            assert t is not None and 1e6 < t < 1e11, (cfg, t)
+            found += 1
+        if os.path.exists(os.path.join(root, "profiles", f"mfma_{cfg}.md")):
+            for ph in ("leaf_forward", "leaf_backward"):
+                fr = bench.read_profile("mfma", "mfma_counter_frac", ph, cfg)
+                ut = bench.read_profile("mfma", "mfma_util_pct", ph, cfg)
+                if fr is None:  # one-token leaves: no MFMA leaf kernel
+                    continue
+                assert 0 < fr < 1 and 0 < ut < 100, (cfg, ph, fr, ut)
+    assert found >= 1
+    assert bench.read_profile("mfma", "mfma_util_pct", "leaf_backward", "no-such-config") is None
