@@ -268,7 +268,10 @@ def test_seed_path_equals_explicit_uniforms_and_is_deterministic():
 # (L, B, H, D, S) of the reference's own end-to-end parity test
 # (test_harness_smoke.py:824-917); D = 16 runs zero-padded to 32 head dims.
 REFERENCE_E2E_SHAPES = [(8, 1, 2, 16, 4), (32, 2, 2, 16, 4), (64, 1, 8, 16, 4), (128, 1, 2, 64, 8), (512, 2, 4, 32, 8),
-                        (32, 2, 2, 32, 4)]
+                        (32, 2, 2, 32, 4),
+                        # head dims that are not a kernel size nor a multiple of 8 (E % H == 0 is all the
+                        # reference asks, _tree_mha.py:348-351): zero-padded to 32 / 128
+                        (64, 1, 2, 5, 4), (128, 2, 3, 100, 8)]
 
 
 @pytest.mark.parametrize("L,B,H,D,S", REFERENCE_E2E_SHAPES)
@@ -319,6 +322,31 @@ def test_op_level_hierarchical_attention_matches_reference_restatement(L, B, H, 
     assert rel(f64(qd.grad).reshape(L, B, H, D).transpose(1, 0, 2, 3), dq) < 1e-5
     assert rel(f64(kd.grad).reshape(L - 1, B, H, D).transpose(1, 2, 0, 3), dkn) < 1e-5
     assert rel(f64(vd.grad).reshape(L, B, H, D).transpose(1, 0, 2, 3), dv) < 1e-5
+
+
+@pytest.mark.parametrize("D,dtype", [(40, torch.bfloat16), (12, torch.float32)])
+def test_head_dim_padding_is_exact(D, dtype):
+    """A head dim the kernels do not implement runs zero-padded to the next one with the softmax
+    scale of the true D: output and gradients equal the padded problem's, sliced."""
+    import treeattention_amd as ta
+
+    B, L, H, S = 1, 512, 2, 8
+    Dp = 64 if D > 32 else 32
+    print(f"[case] head-dim padding D={D} -> {Dp} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    q, k, v, do = (torch.randn(B, L, H, D, generator=g).to(dtype).cuda() for _ in range(4))
+    kw = dict(num_samples=S, branching=2, leaf_block=16, tree_mode="natural", seed=11)
+    xs = [x.clone().requires_grad_(True) for x in (q, k, v)]
+    out = ta.tree_attention(*xs, True, None, **kw)
+    out.backward(do)
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dp - D))  # noqa: E731
+    ps = [pad(x).requires_grad_(True) for x in (q, k, v)]
+    outp = ta.tree_attention(*ps, True, 1.0 / math.sqrt(D), **kw)
+    outp.backward(pad(do))
+    assert out.shape == (B, L, H, D)
+    assert torch.equal(out, outp[..., :D])
+    for a_, b_ in zip(xs, ps):
+        assert torch.equal(a_.grad, b_.grad[..., :D])
 
 
 def test_op_level_block_size_invariance():

@@ -4,8 +4,9 @@
 // weighted_value_sum.cu:8-47) and the backward needs only
 //   delta_u = dout_l . v[leaf_u]          (per distinct leaf of a query)
 //   dv[n]   = sum_{(l, u) -> n} W_u dout_l   (the leaf's bucket, in order)
-// (scatter_weighted_grad_v.cu:9-54 without atomics); the leaf softmax over one
-// key has no gradient, so there is no leaf dq or dk.
+// (scatter_weighted_grad_v.cu:9-54 without atomics), both in one pass over
+// the leaf buckets; the leaf softmax over one key has no gradient, so there
+// is no leaf dq or dk.
 #include "launch.h"
 
 namespace ta {
@@ -84,60 +85,53 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs a, int bh0, 
   store8f((E*)a.out + bb * a.osb + l * a.osl + h * a.osh + d0, acc);
 }
 
-// delta[qh, u] = dout_l . v[leaf_u]; one thread per (query, slot).
-template <typename E>
-__global__ __launch_bounds__(256) void gather_delta_kernel(GatherArgs a, int64_t nqh) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t qh = gid / a.S;
-  if (qh >= nqh) return;
-  const int u = (int)(gid - qh * a.S);
-  if (u >= a.slot_count[qh]) return;
-  const int64_t h = qh % a.H, bl = qh / a.H, l = bl % a.L, bb = bl / a.L;
-  const int leaf = a.slot_leaf[qh * a.S + u];
-  const E* vr = (const E*)a.v + bb * a.vsb + (int64_t)leaf * a.vsl + h * a.vsh;
-  const E* gr = (const E*)a.g + bb * a.gsb + l * a.gsl + h * a.gsh;
-  float s = 0.f;
-  for (int d0 = 0; d0 < a.D; d0 += 8) {
-    float x[8], y[8];
-    load8f(x, vr + d0);
-    load8f(y, gr + d0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += x[i] * y[i];
-  }
-  a.delta[qh * a.S + u] = s;
-}
-
-// dv[b, n, h, :] = sum over leaf n's bucket (query order) of W_u dout_l; one
-// thread per (leaf, 8 head dims), grid (.., B*H).
-template <typename E>
+// dv[b, n, h, :] = sum over leaf n's bucket (query order) of W_u dout_l, and
+// for every entry (l, u) of the bucket delta[qh, u] = dout_l . v[n] (the
+// leaf's value row is loaded once; the dout rows are the ones dv reads).
+// TP = D / 8 rounded up to a power of two lanes per leaf, 8 head dims each
+// (lanes past D idle), so the dot products reduce with xor shuffles inside
+// the group; grid (.., B*H).
+template <typename E, int TP>
 __global__ __launch_bounds__(256) void scatter_dv_kernel(GatherArgs a) {
-  const int TPQ = a.D / 8;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n = gid / TPQ;
-  if (n >= a.N) return;
-  const int d0 = (int)(gid - n * TPQ) * 8;
+  const int64_t n = gid / TP;
+  if (n >= a.N) return;  // whole groups: TP divides the workgroup size
+  const int d0 = (int)(gid - n * TP) * 8;
+  const bool on = d0 < a.D;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
   const int* bs = a.block_start + (int64_t)bh * (a.N + 1);
   const int* ord = a.order + (int64_t)bh * a.L * a.S;
   const int e0 = bs[n], e1 = bs[n + 1];
-  const E* g = (const E*)a.g + bb * a.gsb + h * a.gsh + d0;
+  const E* g = (const E*)a.g + bb * a.gsb + h * a.gsh + (on ? d0 : 0);
+  float vn[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (on) load8f(vn, (const E*)a.v + bb * a.vsb + n * a.vsl + h * a.vsh + d0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int e = e0; e < e1; e += 4) {
     float x[4][8], w[4];
+    int64_t slot[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool ok = e + j < e1;
       const int ent = ok ? ord[e + j] : 0;
       const int l = ent / a.S, u = ent - l * a.S;
-      w[j] = ok ? a.slot_weight[(((int64_t)bb * a.L + l) * a.H + h) * a.S + u] : 0.f;
+      slot[j] = (((int64_t)bb * a.L + l) * a.H + h) * a.S + u;
+      w[j] = ok ? a.slot_weight[slot[j]] : 0.f;
       load8f(x[j], g + (int64_t)l * a.gsl);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      float dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += w[j] * x[j][i];
+      for (int i = 0; i < 8; ++i) {
+        acc[i] += w[j] * x[j][i];
+        dot += x[j][i] * vn[i];
+      }
+#pragma unroll
+      for (int o = 1; o < TP; o <<= 1) dot += __shfl_xor(dot, o, 64);
+      if (d0 == 0 && e + j < e1) a.delta[slot[j]] = dot;
+    }
   }
-  store8f((E*)a.out + bb * a.osb + n * a.osl + h * a.osh + d0, acc);
+  if (on) store8f((E*)a.out + bb * a.osb + n * a.osl + h * a.osh + d0, acc);
 }
 
 static GatherArgs gather_args(const Plan& P, const void* v, const char* rec) {
@@ -181,13 +175,14 @@ static hipError_t gather_bwd_t(const Plan& P, const void* v, const void* g, void
   a.g = g;
   a.gsb = P.p.g_strides[0]; a.gsl = P.p.g_strides[1]; a.gsh = P.p.g_strides[2];
   a.delta = delta;
-  const int64_t nqh = P.B * P.L * P.H;
-  hipLaunchKernelGGL(gather_delta_kernel<E>, dim3((unsigned)((nqh * P.S + 255) / 256)), dim3(256), 0, st, a, nqh);
   a.out = dv;
   a.osb = P.p.v_strides[0]; a.osl = P.p.v_strides[1]; a.osh = P.p.v_strides[2];
-  const int64_t nthr = P.N * (P.D / 8);
-  hipLaunchKernelGGL(scatter_dv_kernel<E>, dim3((unsigned)((nthr + 255) / 256), (unsigned)P.BH), dim3(256), 0, st,
-                     a);
+  const int tp = P.D <= 32 ? 4 : P.D <= 64 ? 8 : 16;
+  const int64_t nthr = P.N * tp;
+  const dim3 grid((unsigned)((nthr + 255) / 256), (unsigned)P.BH);
+  if (tp == 4) hipLaunchKernelGGL((scatter_dv_kernel<E, 4>), grid, dim3(256), 0, st, a);
+  else if (tp == 8) hipLaunchKernelGGL((scatter_dv_kernel<E, 8>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((scatter_dv_kernel<E, 16>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

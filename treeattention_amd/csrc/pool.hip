@@ -94,6 +94,8 @@ __global__ __launch_bounds__(256) void seg_sums_kernel(const float* __restrict__
 struct SumArgs {
   Geo geo;
   int H, D, mode;
+  int hilo_lam;         // levels 1 .. hilo_lam are read as MFMA tiles: hi, lo copies
+  int t_lam;            // levels 1 .. t_lam also as the transposed copy
   const float* means;   // (BH, NL, D)
   const float* seg1;    // (BH, NL / kSeg, D) or null
   const float* seg2;    // (BH, NL / kSeg^2, D) or null
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
     const int64_t row_off = ((int64_t)bh * rows + r) * D + d0;
     *(float4*)(a.sum32 + row_off) = make_float4(val[0], val[1], val[2], val[3]);
     *(float4*)(a.sum32 + row_off + 4) = make_float4(val[4], val[5], val[6], val[7]);
+    if (lam > a.hilo_lam) continue;  // per-path levels read the float rows only
     float* tr = tile + rr * (128 + 4) + d0;
     if constexpr (sizeof(E) == 2) {
       typedef __attribute__((ext_vector_type(8))) E e8;
@@ -204,6 +207,7 @@ __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
       for (int j = 0; j < 8; ++j) tr[j] = val[j];
     }
   }
+  if (lam > a.t_lam) return;  // uniform: a tile never spans two levels
   __syncthreads();
   // transposed copy: (bh, d, r0 .. r0 + 31), eight rows per store
   for (int e = threadIdx.x; e < D * (kSumRows / 8); e += blockDim.x) {
@@ -248,6 +252,11 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   a.H = (int)P.H;
   a.D = (int)P.D;
   a.mode = P.p.tree_mode;
+  // level lam holds the children of depth lam - 1 nodes: MFMA tiles in the
+  // sampler below depth sample_dense (and, causal, the boundary nodes' children
+  // at every depth), in the tree backward below tree_dense (also transposed)
+  a.t_lam = P.tree_dense;
+  a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT ? G.T : (P.sample_dense > P.tree_dense ? P.sample_dense : P.tree_dense);
   a.means = means;
   a.knodes = k;
   a.ksb = P.p.k_strides[0];
