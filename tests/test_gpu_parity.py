@@ -216,6 +216,12 @@ def test_odd_leaf_blocks_and_partial_query_tiles(b, LB, L, D, causal, dtype):
     run_case(2, L, 2, D, 8, b, LB, "natural", causal, dtype)
 
 
+@pytest.mark.parametrize("D,LB,causal", [(128, 64, True), (96, 128, False), (64, 128, True)])
+def test_float_large_leaf_tiles(D, LB, causal):
+    # fp32 with large head dims / blocks: the leaf backward's 32- and 16-pair tiles
+    run_case(1, 16 * LB, 2, D, 8, 2, LB, "natural", causal, torch.float32)
+
+
 def test_large_bucket_histogram():
     # 2048 leaf blocks (one counting-sort window) x 64 query chunks: the bucket
     # counts are scanned in segments by several workgroups per (batch, head)

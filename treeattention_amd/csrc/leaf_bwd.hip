@@ -49,19 +49,30 @@ __device__ __forceinline__ void zero8e(E* o) {
   }
 }
 
-// K^T is kept in LDS (for the dq product) when it fits next to the rest.
+// Pair tiles of QT = 64 pairs (16 per wave in phase A) with K^T kept in LDS
+// for the dq product when it fits; where the K / V block, the tile's rows and
+// its (wP)^T, dz^T tiles would exceed the 160 KiB of LDS (float inputs with
+// large head dims or blocks) the tile shrinks to 32 or 16 pairs, phase A on
+// the first QT / 16 waves, and K^T is read from the K rows instead.
 template <int D, int LBP, int ES>
 struct BwdTile {
-  static constexpr int RS = D + 8, PS = 64 + 8, TS = LBP + 8;  // padded LDS row strides
-  static constexpr bool kKt = (LBP <= 64) || ES == 2 && D <= 64;
-  static constexpr int bytes = (2 * LBP * RS + 2 * 64 * RS + 2 * LBP * PS + (kKt ? D * TS : 0)) * ES + 64 * 4;
+  static constexpr int RS = D + 8, TS = LBP + 8;  // padded LDS row strides
+  static constexpr int bytes_for(int qt, bool kt) {
+    return (2 * LBP * RS + 2 * qt * RS + 2 * LBP * (qt + 8) + (kt ? D * TS : 0)) * ES + 64 * 4;
+  }
+  static constexpr bool kKt64 = (LBP <= 64) || ES == 2 && D <= 64;
+  static constexpr int kMax = 160 * 1024;
+  static constexpr int QT = bytes_for(64, kKt64) <= kMax ? 64 : bytes_for(32, false) <= kMax ? 32 : 16;
+  static constexpr bool kKt = QT == 64 && kKt64;
+  static constexpr int PS = QT + 8;
+  static constexpr int bytes = bytes_for(QT, kKt);
 };
 
 template <typename E, int D, int LBP>
 __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   using M = Mfma<E>;
   using BT = BwdTile<D, LBP, (int)sizeof(E)>;
-  constexpr int QT = 64, RS = BT::RS, PS = BT::PS, TS = BT::TS;
+  constexpr int QT = BT::QT, RS = BT::RS, PS = BT::PS, TS = BT::TS;
   constexpr int NT = (LBP / 16) * (D / 16) / 4;  // dV / dK tiles per wave
   extern __shared__ __align__(16) char smem[];
   E* Ks = (E*)smem;        // [LBP][RS]
@@ -121,6 +132,7 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
     }
     __syncthreads();
 
+    if (16 * w < QT) {  // phase A: this wave's 16 pairs of the tile
     const int qcol = 16 * w + col;
     const int ent = ent_s[qcol];
     const bool valid = ent >= 0;
@@ -202,6 +214,7 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
           o = M::mma(ld_frag_perm_strided<E>(Ks + 16 * md + col, RS, ks, g), acc_operand<E>(pacc, ks), o);
       }
       if (valid) store4(dqp + 16 * md + 4 * g, o, a.scale);
+    }
     }
     __syncthreads();
 
@@ -547,8 +560,17 @@ int leaf_bwd_smem(const Plan& P) {
     const int s = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
     return s <= 160 * 1024 ? s : -1;
   }
-  const bool kt = LBP <= 64;
-  const int s = (2 * LBP * (D + 8) + 2 * 64 * (D + 8) + 2 * LBP * 72 + (kt ? D * (LBP + 8) : 0)) * ES + 64 * 4;
+  int s = 0;
+  switch (D * 1000 + LBP) {
+#define TA_BWD_TILE(d, lbp) \
+  case d * 1000 + lbp: s = ES == 2 ? BwdTile<d, lbp, 2>::bytes : BwdTile<d, lbp, 4>::bytes; break;
+    TA_BWD_TILE(32, 32) TA_BWD_TILE(32, 64) TA_BWD_TILE(32, 128)
+    TA_BWD_TILE(64, 32) TA_BWD_TILE(64, 64) TA_BWD_TILE(64, 128)
+    TA_BWD_TILE(96, 32) TA_BWD_TILE(96, 64) TA_BWD_TILE(96, 128)
+    TA_BWD_TILE(128, 32) TA_BWD_TILE(128, 64) TA_BWD_TILE(128, 128)
+#undef TA_BWD_TILE
+    default: return -1;
+  }
   return s <= 160 * 1024 ? s : -1;
 }
 
