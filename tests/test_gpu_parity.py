@@ -216,9 +216,10 @@ def test_odd_leaf_blocks_and_partial_query_tiles(b, LB, L, D, causal, dtype):
     run_case(2, L, 2, D, 8, b, LB, "natural", causal, dtype)
 
 
-@pytest.mark.parametrize("D,LB,causal", [(128, 64, True), (96, 128, False), (64, 128, True)])
+@pytest.mark.parametrize("D,LB,causal", [(128, 64, True), (96, 128, False), (64, 128, True), (128, 128, True)])
 def test_float_large_leaf_tiles(D, LB, causal):
-    # fp32 with large head dims / blocks: the leaf backward's 32- and 16-pair tiles
+    # fp32 with large head dims / blocks: the leaf backward's 32- and 16-pair tiles (D=128, LB=128:
+    # V operands from global memory)
     run_case(1, 16 * LB, 2, D, 8, 2, LB, "natural", causal, torch.float32)
 
 

@@ -56,10 +56,10 @@ def test_struct_layout_and_sizes():
     assert ns == 32 + 32 + 64 + 256  # levels 4, 16, 64, 256 padded to 32 rows
 
 
-@pytest.mark.parametrize("D,LB", [(128, 64), (96, 64), (96, 128), (64, 128), (32, 128)])
+@pytest.mark.parametrize("D,LB", [(128, 64), (96, 64), (96, 128), (64, 128), (32, 128), (128, 128)])
 def test_float_leaf_tiles_fit(D, LB):
     """fp32 inputs with large head dims or blocks run the leaf backward with 32- or 16-pair
-    tiles instead of being refused."""
+    tiles (D=128 at LB=128: V read from global memory) instead of being refused."""
     N = LB * 2 ** 8
     _lib.byte_sizes(_problem(dtype=_lib.TA_F32, D=D, leaf_block=LB, N=N, L=N, branching=2, causal=0))
 
@@ -68,7 +68,6 @@ def test_float_leaf_tiles_fit(D, LB):
     (dict(D=80), NotImplementedError),
     (dict(num_samples=65), NotImplementedError),
     (dict(leaf_block=256), NotImplementedError),
-    (dict(dtype=_lib.TA_F32, leaf_block=128, N=16384 * 2, causal=0), NotImplementedError),  # fp32 D=128 LB=128 tile
     (dict(N=16384 + 64, L=16384 + 64), ValueError),  # not leaf_block * b^T
     (dict(branching=3), ValueError),
     (dict(tree_mode=_lib.TA_TREE_COMPAT), ValueError),  # compat is binary

@@ -54,18 +54,24 @@ __device__ __forceinline__ void zero8e(E* o) {
 // its (wP)^T, dz^T tiles would exceed the 160 KiB of LDS (float inputs with
 // large head dims or blocks) the tile shrinks to 32 or 16 pairs, phase A on
 // the first QT / 16 waves, and K^T is read from the K rows instead.
+// When even 16-pair tiles do not fit (float, head dim 128, 128-key blocks),
+// V stays in global memory (L2-resident, 64 KB per block) and phase A reads
+// its MFMA operands from there: 32-pair tiles.
 template <int D, int LBP, int ES>
 struct BwdTile {
   static constexpr int RS = D + 8, TS = LBP + 8;  // padded LDS row strides
-  static constexpr int bytes_for(int qt, bool kt) {
-    return (2 * LBP * RS + 2 * qt * RS + 2 * LBP * (qt + 8) + (kt ? D * TS : 0)) * ES + 64 * 4;
+  static constexpr int bytes_for(int qt, bool kt, bool vs) {
+    return ((vs ? 2 : 1) * LBP * RS + 2 * qt * RS + 2 * LBP * (qt + 8) + (kt ? D * TS : 0)) * ES + 64 * 4;
   }
   static constexpr bool kKt64 = (LBP <= 64) || ES == 2 && D <= 64;
   static constexpr int kMax = 160 * 1024;
-  static constexpr int QT = bytes_for(64, kKt64) <= kMax ? 64 : bytes_for(32, false) <= kMax ? 32 : 16;
-  static constexpr bool kKt = QT == 64 && kKt64;
+  static constexpr bool kVg = bytes_for(16, false, true) > kMax;  // V read from global memory
+  static constexpr int QT = kVg ? 32
+                            : bytes_for(64, kKt64, true) <= kMax ? 64
+                            : bytes_for(32, false, true) <= kMax ? 32 : 16;
+  static constexpr bool kKt = QT == 64 && kKt64 && !kVg;
   static constexpr int PS = QT + 8;
-  static constexpr int bytes = bytes_for(QT, kKt);
+  static constexpr int bytes = bytes_for(QT, kKt, !kVg);
 };
 
 template <typename E, int D, int LBP>
@@ -76,8 +82,8 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   constexpr int NT = (LBP / 16) * (D / 16) / 4;  // dV / dK tiles per wave
   extern __shared__ __align__(16) char smem[];
   E* Ks = (E*)smem;        // [LBP][RS]
-  E* Vs = Ks + LBP * RS;   // [LBP][RS]
-  E* Qs = Vs + LBP * RS;   // [QT][RS]
+  E* Vs = Ks + LBP * RS;   // [LBP][RS] (unless kVg)
+  E* Qs = Vs + (BT::kVg ? 0 : LBP * RS);  // [QT][RS]
   E* Gs = Qs + QT * RS;    // [QT][RS]
   E* Pt = Gs + QT * RS;    // [LBP][PS]  (w P)^T
   E* Zt = Pt + LBP * PS;   // [LBP][PS]  dz^T
@@ -102,8 +108,10 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
     const int64_t tok = (int64_t)beta * LB + key;
     if (key < LB && k) mov8(Ks + key * RS + c, k + bb * a.ksb + tok * a.ksl + h * a.ksh + c);
     else zero8e(Ks + key * RS + c);
-    if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
-    else zero8e(Vs + key * RS + c);
+    if constexpr (!BT::kVg) {
+      if (key < LB) mov8(Vs + key * RS + c, v + bb * a.vsb + tok * a.vsl + h * a.vsh + c);
+      else zero8e(Vs + key * RS + c);
+    }
     if constexpr (BT::kKt) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) Kt[(c + i) * TS + key] = Ks[key * RS + c + i];
@@ -145,13 +153,26 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
       sacc[mt] = zero4();
       pacc[mt] = zero4();
       const E* kp = Ks + (16 * mt + col) * RS + M::KPL * g;
-      const E* vp = Vs + (16 * mt + col) * RS + M::KPL * g;
       const E* qp = Qs + qcol * RS + M::KPL * g;
       const E* gp = Gs + qcol * RS + M::KPL * g;
+      if constexpr (BT::kVg) {
+        // V rows from global memory (keys past LB are zero)
+        const int key = 16 * mt + col;
+        const E* vg = v + bb * a.vsb + ((int64_t)beta * LB + (key < LB ? key : 0)) * a.vsl + h * a.vsh + M::KPL * g;
+        const bool kin = key < LB;
 #pragma unroll
-      for (int ks = 0; ks < D / M::K; ++ks) {
-        sacc[mt] = M::mma(ld_frag(kp + ks * M::K), ld_frag(qp + ks * M::K), sacc[mt]);
-        pacc[mt] = M::mma(ld_frag(vp + ks * M::K), ld_frag(gp + ks * M::K), pacc[mt]);
+        for (int ks = 0; ks < D / M::K; ++ks) {
+          sacc[mt] = M::mma(ld_frag(kp + ks * M::K), ld_frag(qp + ks * M::K), sacc[mt]);
+          const E vv = kin ? vg[ks * M::K] : (E)0.f;
+          pacc[mt] = M::mma(vv, ld_frag(gp + ks * M::K), pacc[mt]);
+        }
+      } else {
+        const E* vp = Vs + (16 * mt + col) * RS + M::KPL * g;
+#pragma unroll
+        for (int ks = 0; ks < D / M::K; ++ks) {
+          sacc[mt] = M::mma(ld_frag(kp + ks * M::K), ld_frag(qp + ks * M::K), sacc[mt]);
+          pacc[mt] = M::mma(ld_frag(vp + ks * M::K), ld_frag(gp + ks * M::K), pacc[mt]);
+        }
       }
     }
     const int kmax = valid ? (a.causal ? min(LB, l + (a.N - a.L) - beta * LB + 1) : LB) : 0;
