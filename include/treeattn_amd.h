@@ -63,7 +63,9 @@ typedef struct ta_problem {
   int64_t B, L, H, D;    /* batch, query positions, heads, head dim */
   int64_t N;             /* leaf tokens (keys/values); N = leaf_block * b^T.  Causal masks are
                             bottom-right aligned: query t sees tokens <= t + N - L (needs L <= N) */
-  int64_t num_samples;   /* S: sampled paths per query, 1..64 */
+  int64_t num_samples;   /* S: sampled paths per query, 1..64 for every entry point; ta_forward,
+                            ta_forward_replay and ta_backward take up to 1024 (non-reference
+                            causal modes), drawn and used in chunks of at most 64 */
   int64_t branching;     /* b >= 2 */
   int64_t leaf_block;    /* LB >= 1 */
   int32_t tree_mode;     /* TA_TREE_* */

@@ -64,9 +64,28 @@ def test_float_leaf_tiles_fit(D, LB):
     _lib.byte_sizes(_problem(dtype=_lib.TA_F32, D=D, leaf_block=LB, N=N, L=N, branching=2, causal=0))
 
 
+def test_many_samples_run_in_chunks():
+    """More than 64 samples: the record holds one chunk record per <= 64 samples plus every
+    sample's leaf block and the float output; workspaces are reused chunk after chunk."""
+    one = _lib.byte_sizes(_problem(num_samples=64))
+    two = _lib.byte_sizes(_problem(num_samples=128))
+    assert two[0] > 2 * one[0]          # two chunk records + leaves + float output
+    assert two[1] == one[1]             # chunks of 64: the same forward workspace
+    assert two[2] > one[2]              # + float accumulators
+    lo = _lib.record_offset(_problem(num_samples=128), _lib.TA_REC_LEAVES)
+    assert lo + 2 * 16384 * 16 * 128 * 4 <= two[0]
+    _lib.byte_sizes(_problem(num_samples=1024))
+    _lib.byte_sizes(_problem(num_samples=100, causal=0))
+    # the per-phase entry points take one launch's worth
+    lib = _lib.load()
+    rc = lib.ta_bucket(ctypes.byref(_problem(num_samples=65)), None, None)
+    assert rc != 0 and b"ta_forward" in lib.ta_last_error()
+
+
 @pytest.mark.parametrize("kw,exc", [
     (dict(D=80), NotImplementedError),
-    (dict(num_samples=65), NotImplementedError),
+    (dict(num_samples=1025), NotImplementedError),
+    (dict(num_samples=65, causal=2, branching=2, leaf_block=1, tree_mode=_lib.TA_TREE_COMPAT), NotImplementedError),
     (dict(leaf_block=256), NotImplementedError),
     (dict(N=16384 + 64, L=16384 + 64), ValueError),  # not leaf_block * b^T
     (dict(branching=3), ValueError),

@@ -60,7 +60,9 @@ int make_plan(const ta_problem* p, Plan* P) {
   if (D != 32 && D != 64 && D != 96 && D != 128)
     return fail(TA_ERR_UNSUPPORTED, "head_dim must be one of 32, 64, 96, 128 (got %lld)", (long long)D);
   if (S < 1 || S > kMaxSamples)
-    return fail(TA_ERR_UNSUPPORTED, "num_samples must be in [1, %d] (got %lld)", kMaxSamples, (long long)S);
+    return fail(TA_ERR_UNSUPPORTED,
+                "num_samples must be in [1, %d] for one launch (got %lld); ta_forward and ta_backward take up to %d",
+                kMaxSamples, (long long)S, kMaxChunks * kMaxSamples);
   if (b < 2 || b > 64 || (b & (b - 1)))
     return fail(TA_ERR_INVALID, "branching must be a power of two in [2, 64] (got %lld)", (long long)b);
   if (LB < 1 || LB > 128) return fail(TA_ERR_UNSUPPORTED, "leaf_block must be in [1, 128] (got %lld)", (long long)LB);
@@ -96,6 +98,9 @@ int make_plan(const ta_problem* p, Plan* P) {
     return fail(TA_ERR_UNSUPPORTED, "tensor strides must be multiples of 8 elements");
 
   P->B = B; P->L = L; P->N = N; P->H = H; P->D = D; P->S = S; P->BH = B * H;
+  P->s0 = 0;
+  P->s_total = S;
+  memset(&P->acc, 0, sizeof(P->acc));
   P->esize = p->dtype == TA_F32 ? 4 : 2;
   Geo& G = P->geo;
   memset(&G, 0, sizeof(G));
@@ -175,6 +180,7 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.slot_leaf = r.take(BLHS * 4);
   P->rec.slot_weight = r.take(BLHS * 4);
   P->rec.slot_count = r.take(B * L * H * 4);
+  P->rec.lse = r.take(B * L * H * 4);
   P->rec.hist = r.take(P->BH * NL * P->nchunk * 4);
   P->rec.block_start = r.take(P->BH * (NL + 1) * 4);
   P->rec.order = r.take(P->BH * L * S * 4);
@@ -217,6 +223,64 @@ int make_plan(const ta_problem* p, Plan* P) {
   return TA_OK;
 }
 
+int make_chunks(const ta_problem* p, Chunks* C) {
+  if (!p) return fail(TA_ERR_INVALID, "problem is NULL");
+  const int64_t S = p->num_samples;
+  if (S <= kMaxSamples) {
+    C->n = 1;
+    const int rc = make_plan(p, &C->P[0]);
+    if (rc) return rc;
+    const Plan& P = C->P[0];
+    C->rec_off[0] = 0;
+    C->rec_leaf = P.rec.leaf;
+    C->rec_out32 = -1;
+    C->rec_total = P.rec.total;
+    C->fws_total = P.fws.total;
+    C->bws_dq32 = C->bws_dv32 = C->bws_dkl = C->bws_dsum = C->bws_mean = -1;
+    C->bws_chunk = 0;
+    C->bws_total = P.bws.total;
+    return TA_OK;
+  }
+  if (S > (int64_t)kMaxChunks * kMaxSamples)
+    return fail(TA_ERR_UNSUPPORTED, "num_samples must be in [1, %d] (got %lld)", kMaxChunks * kMaxSamples,
+                (long long)S);
+  if (p->causal == TA_CAUSAL_REFERENCE)
+    return fail(TA_ERR_UNSUPPORTED, "the reference causal mode couples every sample of a query in one workgroup; "
+                                    "num_samples must be <= %d there (got %lld)", kMaxSamples, (long long)S);
+  const int n = (int)((S + kMaxSamples - 1) / kMaxSamples);
+  C->n = n;
+  Carver r, w;
+  int64_t fws = 0, bws = 0, s0 = 0;
+  for (int g = 0; g < n; ++g) {
+    ta_problem pg = *p;
+    pg.num_samples = S / n + (g < S % n ? 1 : 0);
+    const int rc = make_plan(&pg, &C->P[g]);
+    if (rc) return rc;
+    Plan& P = C->P[g];
+    P.s0 = s0;
+    P.s_total = S;
+    s0 += pg.num_samples;
+    C->rec_off[g] = r.take(P.rec.total);
+    fws = fws > P.fws.total ? fws : P.fws.total;
+    bws = bws > P.bws.total ? bws : P.bws.total;
+  }
+  const Plan& P0 = C->P[0];
+  const int64_t BLH = P0.B * P0.L * P0.H, BNH = P0.B * P0.N * P0.H, D = P0.D;
+  C->rec_leaf = r.take(BLH * S * 4);
+  C->rec_out32 = r.take(BLH * D * 4);
+  C->rec_total = r.at;
+  C->fws_total = fws;
+  C->bws_dq32 = w.take(BLH * D * 4);
+  C->bws_dv32 = w.take(BNH * D * 4);
+  const bool dkl = P0.geo.LB > 1 && p->tree_mode != TA_TREE_NODEKEYS;  // the leaf stage has a dk part
+  C->bws_dkl = w.take(dkl ? BNH * D * 4 : 0);
+  C->bws_dsum = w.take(P0.BH * P0.geo.NS * D * 4);
+  C->bws_mean = w.take(BLH * 4);
+  C->bws_chunk = w.take(bws);
+  C->bws_total = w.at;
+  return TA_OK;
+}
+
 namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -224,6 +288,106 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int launch_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(TA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+}  // namespace ta
+
+namespace ta {
+namespace {
+
+// Forward of a problem with more samples than one launch: every chunk's pool
+// and sampler, the merge of the chunks' normalizers, then every chunk's
+// bucketing and leaf stage adding into the float output, rounded once.
+int forward_chunks(const ta_problem* p, const void* q, const void* k, const void* v, const float* U, uint64_t seed,
+                   const uint8_t* packed, void* out, float* weights, void* record, void* workspace, void* stream) {
+  static thread_local Chunks C;
+  int rc = make_chunks(p, &C);
+  if (rc) return rc;
+  const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
+  const bool need_ws = C.fws_total > 0;  // leaf_block 1 needs none
+  if (!q || !v || !out || !weights || !record || (need_ws && !workspace) || (need_k && !k) || !aligned16(q) ||
+      !aligned16(v) || !aligned16(out) || !aligned16(record) || !aligned16(workspace) || (need_k && !aligned16(k)))
+    return fail(TA_ERR_INVALID, "q/k/v/out/weights/record/workspace must be 16-byte aligned device pointers");
+  hipStream_t st = (hipStream_t)stream;
+  char* rec = (char*)record;
+  ChunkRecs R;
+  R.n = C.n;
+  for (int g = 0; g < C.n; ++g) {
+    const Plan& P = C.P[g];
+    char* rg = rec + C.rec_off[g];
+    hipError_t e = launch_pool(P, k, rg, st);
+    if (e != hipSuccess) return launch_status(e, "pool");
+    e = launch_sample(P, q, U, seed, weights + P.s0, rg, st, packed);
+    if (e != hipSuccess) return launch_status(e, packed ? "replay" : "sample");
+    R.S[g] = (int)P.S;
+    R.s0[g] = (int)P.s0;
+    R.lse[g] = (const float*)(rg + P.rec.lse);
+    R.slot_weight[g] = (float*)(rg + P.rec.slot_weight);
+    R.slot_count[g] = (const int*)(rg + P.rec.slot_count);
+    R.leaf[g] = (const int*)(rg + P.rec.leaf);
+  }
+  hipError_t e = launch_chunk_merge(C.P[0], R, weights, (int*)(rec + C.rec_leaf), st);
+  if (e != hipSuccess) return launch_status(e, "chunk_merge");
+  float* out32 = (float*)(rec + C.rec_out32);
+  for (int g = 0; g < C.n; ++g) {
+    Plan P = C.P[g];
+    char* rg = rec + C.rec_off[g];
+    e = launch_bucket(P, rg, st);
+    if (e != hipSuccess) return launch_status(e, "bucket");
+    P.acc.out32 = out32;
+    P.acc.first = g == 0;
+    e = launch_leaf_fwd(P, q, k, v, out, rg, (char*)workspace, st);
+    if (e != hipSuccess) return launch_status(e, "leaf_forward");
+  }
+  const Plan& P0 = C.P[0];
+  return launch_status(launch_cast_rows(p->dtype, out32, out, p->o_strides, P0.B, P0.L, P0.H, P0.D, st), "cast");
+}
+
+// Backward of a chunked problem: mean = dout . out over all samples, then per
+// chunk the leaf and tree backward (dl_u = W_u (delta_u - mean), W the
+// weights over all samples) adding into float accumulators; the last chunk
+// runs the key adjoint from the summed leaf dk and summary gradient.
+int backward_chunks(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
+                    const float* weights, const void* record, void* dq, void* dk, void* dv, void* workspace,
+                    void* stream) {
+  static thread_local Chunks C;
+  int rc = make_chunks(p, &C);
+  if (rc) return rc;
+  const bool need_k = p->tree_mode != TA_TREE_NODEKEYS;
+  if (!q || !v || !grad_out || !weights || !record || !dq || !dk || !dv || !workspace || (need_k && !k))
+    return fail(TA_ERR_INVALID, "NULL device pointer");
+  const void* al[] = {q, v, grad_out, record, dq, dk, dv, workspace};
+  for (const void* x : al)
+    if (!aligned16(x)) return fail(TA_ERR_INVALID, "device pointers must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const char* rec = (const char*)record;
+  char* ws = (char*)workspace;
+  ChunkAcc acc;
+  acc.out32 = nullptr;
+  acc.dq32 = (float*)(ws + C.bws_dq32);
+  acc.dv32 = (float*)(ws + C.bws_dv32);
+  acc.dk_leaf = (float*)(ws + C.bws_dkl);
+  acc.dsum = (float*)(ws + C.bws_dsum);
+  acc.mean = (const float*)(ws + C.bws_mean);
+  const Plan& P0 = C.P[0];
+  hipError_t e = launch_chunk_mean(P0, grad_out, (const float*)(rec + C.rec_out32), (float*)(ws + C.bws_mean), st);
+  if (e != hipSuccess) return launch_status(e, "chunk_mean");
+  for (int g = 0; g < C.n; ++g) {
+    Plan P = C.P[g];
+    P.acc = acc;
+    P.acc.first = g == 0;
+    P.acc.last = g == C.n - 1;
+    const char* rg = rec + C.rec_off[g];
+    char* wg = ws + C.bws_chunk;
+    e = launch_leaf_bwd(P, q, k, v, grad_out, rg, dv, wg, st);
+    if (e != hipSuccess) return launch_status(e, "leaf_backward");
+    e = launch_tree_bwd(P, q, weights, rg, dq, dk, wg, st);
+    if (e != hipSuccess) return launch_status(e, "tree_backward");
+  }
+  e = launch_cast_rows(p->dtype, acc.dq32, dq, p->q_strides, P0.B, P0.L, P0.H, P0.D, st);
+  if (e != hipSuccess) return launch_status(e, "cast");
+  return launch_status(launch_cast_rows(p->dtype, acc.dv32, dv, p->v_strides, P0.B, P0.N, P0.H, P0.D, st), "cast");
 }
 
 }  // namespace
@@ -238,40 +402,41 @@ int ta_version(void) { return TA_VERSION; }
 const char* ta_last_error(void) { return last_error(); }
 
 int ta_record_bytes(const ta_problem* p, int64_t* bytes) {
-  Plan P;
-  const int rc = make_plan(p, &P);
+  static thread_local Chunks C;
+  const int rc = make_chunks(p, &C);
   if (rc) return rc;
   if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
-  *bytes = P.rec.total;
+  *bytes = C.rec_total;
   return ok();
 }
 
 int ta_forward_workspace_bytes(const ta_problem* p, int64_t* bytes) {
-  Plan P;
-  const int rc = make_plan(p, &P);
+  static thread_local Chunks C;
+  const int rc = make_chunks(p, &C);
   if (rc) return rc;
   if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
-  *bytes = P.fws.total;
+  *bytes = C.fws_total;
   return ok();
 }
 
 int ta_backward_workspace_bytes(const ta_problem* p, int64_t* bytes) {
-  Plan P;
-  const int rc = make_plan(p, &P);
+  static thread_local Chunks C;
+  const int rc = make_chunks(p, &C);
   if (rc) return rc;
   if (!bytes) return fail(TA_ERR_INVALID, "bytes is NULL");
-  *bytes = P.bws.total;
+  *bytes = C.bws_total;
   return ok();
 }
 
 int ta_record_offset(const ta_problem* p, int which, int64_t* offset) {
-  Plan P;
-  const int rc = make_plan(p, &P);
+  static thread_local Chunks C;
+  const int rc = make_chunks(p, &C);
   if (rc) return rc;
   if (!offset) return fail(TA_ERR_INVALID, "offset is NULL");
+  const Plan& P = C.P[0];
   switch (which) {
-    case TA_REC_LEAVES: *offset = P.rec.leaf; break;
-    case TA_REC_SUMMARIES: *offset = P.rec.summaries; break;
+    case TA_REC_LEAVES: *offset = C.rec_leaf; break;
+    case TA_REC_SUMMARIES: *offset = C.rec_off[0] + P.rec.summaries; break;
     case TA_REC_NUM_ROWS: *offset = P.geo.NS; break;
     default: return fail(TA_ERR_INVALID, "unknown record piece %d", which);
   }
@@ -325,13 +490,16 @@ int ta_leaf_forward(const ta_problem* p, const void* q, const void* k, const voi
 
 int ta_forward(const ta_problem* p, const void* q, const void* k, const void* v, const float* uniforms, uint64_t seed,
                void* out, float* weights, void* record, void* workspace, void* stream) {
-  int rc = ta_pool(p, k, record, stream);
-  if (rc) return rc;
-  rc = ta_sample(p, q, uniforms, seed, weights, record, stream);
-  if (rc) return rc;
-  rc = ta_bucket(p, record, stream);
-  if (rc) return rc;
-  return ta_leaf_forward(p, q, k, v, out, record, workspace, stream);
+  if (p && p->num_samples <= kMaxSamples) {
+    int rc = ta_pool(p, k, record, stream);
+    if (rc) return rc;
+    rc = ta_sample(p, q, uniforms, seed, weights, record, stream);
+    if (rc) return rc;
+    rc = ta_bucket(p, record, stream);
+    if (rc) return rc;
+    return ta_leaf_forward(p, q, k, v, out, record, workspace, stream);
+  }
+  return forward_chunks(p, q, k, v, uniforms, seed, nullptr, out, weights, record, workspace, stream);
 }
 
 int ta_leaf_backward(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
@@ -368,6 +536,8 @@ int ta_tree_backward(const ta_problem* p, const void* q, const float* weights, c
 int ta_backward(const ta_problem* p, const void* q, const void* k, const void* v, const void* grad_out,
                 const float* weights, const void* record, void* dq, void* dk, void* dv, void* workspace,
                 void* stream) {
+  if (p && p->num_samples > kMaxSamples)
+    return backward_chunks(p, q, k, v, grad_out, weights, record, dq, dk, dv, workspace, stream);
   Plan P;
   const int rc = make_plan(p, &P);
   if (rc) return rc;
@@ -591,6 +761,12 @@ int ta_replay(const ta_problem* p, const void* q, const uint8_t* packed, float* 
 
 int ta_forward_replay(const ta_problem* p, const void* q, const void* k, const void* v, const uint8_t* packed,
                       void* out, float* weights, void* record, void* workspace, void* stream) {
+  if (p && p->num_samples > kMaxSamples) {
+    if (p->causal != TA_CAUSAL_NONE)
+      return fail(TA_ERR_UNSUPPORTED, "path replay is for non-causal problems (as the reference's replay)");
+    if (!packed) return fail(TA_ERR_INVALID, "packed paths must be a device pointer");
+    return forward_chunks(p, q, k, v, nullptr, 0, packed, out, weights, record, workspace, stream);
+  }
   int rc = ta_pool(p, k, record, stream);
   if (rc) return rc;
   rc = ta_replay(p, q, packed, weights, record, stream);

@@ -177,6 +177,19 @@ __device__ __forceinline__ typename Mfma<E>::frag acc_operand(const f32x4 (&acc)
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// dst[0..8) = v (first) or dst + v: float rows summed over the sample chunks
+// of a problem with many samples (16-byte aligned dst).
+__device__ __forceinline__ void acc8f(float* dst, const float* v, int first) {
+  float4 a = make_float4(v[0], v[1], v[2], v[3]), b = make_float4(v[4], v[5], v[6], v[7]);
+  if (!first) {
+    const float4 x = *(const float4*)dst, y = *(const float4*)(dst + 4);
+    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+    b.x += y.x; b.y += y.y; b.z += y.z; b.w += y.w;
+  }
+  *(float4*)dst = a;
+  *(float4*)(dst + 4) = b;
+}
+
 // dst[0..4) = scale * v as E, one 8-byte (16-bit E) or 16-byte (float) store;
 // dst must be aligned to 4 elements.
 template <typename E>
@@ -516,6 +529,7 @@ struct RecordLayout {
   int64_t slot_leaf;   // int (B, L, H, S): distinct leaf blocks, ascending
   int64_t slot_weight; // float (B, L, H, S): summed weight per distinct leaf block
   int64_t slot_count;  // int (B, L, H)
+  int64_t lse;         // float (B, L, H): log of the summed exp(log-prob) over the query's samples
   int64_t hist;        // int (BH, NL, nchunk): pair counts, then scanned offsets
   int64_t block_start; // int (BH, NL + 1)
   int64_t order;       // int (BH, L*S): (l*S + u) grouped by leaf block

@@ -5,6 +5,21 @@
 
 namespace ta {
 
+// A problem with more samples than one launch takes (kMaxSamples) runs as
+// chunks of samples, each a plan of its own; these float accumulators in the
+// caller's record / workspace carry the sums across the chunks (all null for
+// a single-chunk problem).  The first chunk writes them, later chunks add in
+// chunk order (deterministic), and the last chunk runs the key adjoint.
+struct ChunkAcc {
+  float* out32;       // (B, L, H, D) forward output
+  float* dq32;        // (B, L, H, D)
+  float* dv32;        // (B, N, H, D)
+  float* dk_leaf;     // (B, N, H, D) leaf-attention part of dk
+  float* dsum;        // (BH, NS, D) summary gradient
+  const float* mean;  // (B, L, H) dout . out over every sample of the query
+  int first, last;
+};
+
 // Everything derived from a ta_problem that the launchers need.
 struct Plan {
   ta_problem p;
@@ -20,13 +35,33 @@ struct Plan {
   int sample_dense; // the sampler's level tiles cover depths < sample_dense; deeper levels are sparse
   int tree_dense;   // the backward's dense G tiles cover depths < tree_dense; deeper ones run in bands
   int bucket_sort;  // many leaf blocks: bucketing by a radix sort of (batch * head, leaf block) keys
+  int64_t s0, s_total;  // this plan's samples are s0 .. s0 + S - 1 of s_total (uniform / path indices)
+  ChunkAcc acc;
   RecordLayout rec;
   FwdWorkspaceLayout fws;
   BwdWorkspaceLayout bws;
 };
 
+// A problem's chunks of samples: num_samples <= kMaxSamples is one chunk
+// whose plan is the problem's own.  With more samples chunk g takes samples
+// s0_g .. s0_g + S_g - 1 (sizes within one of each other), has a record of
+// its own inside the caller's record, and reuses one forward / backward
+// workspace after the other; the record also holds every sample's leaf block
+// and the float forward output, the backward workspace the accumulators.
+constexpr int kMaxChunks = 16;  // num_samples <= kMaxChunks * kMaxSamples
+struct Chunks {
+  int n;
+  Plan P[kMaxChunks];
+  int64_t rec_off[kMaxChunks];  // chunk g's record
+  int64_t rec_leaf;             // int (B, L, H, S): every sample's leaf block (n > 1)
+  int64_t rec_out32;            // float (B, L, H, D): the forward output before rounding (n > 1)
+  int64_t rec_total, fws_total;
+  int64_t bws_dq32, bws_dv32, bws_dkl, bws_dsum, bws_mean, bws_chunk, bws_total;
+};
+
 // capi.cpp: plan builder and the calling thread's error message
 int make_plan(const ta_problem* p, Plan* P);  // TA_OK or an error code (message set)
+int make_chunks(const ta_problem* p, Chunks* C);
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();  // clears the message, returns TA_OK
 const char* last_error();
@@ -87,6 +122,26 @@ hipError_t launch_det_stream_bwd(int dtype, const void* q, const int64_t* qs, co
                                  const void* kn, const int64_t* ks, const void* v, const int64_t* vs, const float* lse,
                                  const float* delta, float* dq, float* achunk, float* dkn, void* dv,
                                  const int64_t* dvs, int B, int L, int H, int D, int T, int causal, hipStream_t st);
+
+// chunks.hip (more samples than one chunk): after every chunk's sampler, the
+// per-query log-normalizers give each chunk's share alpha_g = exp(lse_g - lse)
+// of the query; the chunk's weights (w + s0_g, caller strides) and the summed
+// weights of its record are scaled by it; every chunk's leaf blocks are copied
+// into leaf_all (B, L, H, S).
+struct ChunkRecs {
+  int n;
+  int S[kMaxChunks], s0[kMaxChunks];
+  const float* lse[kMaxChunks];  // pieces of chunk g's record
+  float* slot_weight[kMaxChunks];
+  const int* slot_count[kMaxChunks];
+  const int* leaf[kMaxChunks];
+};
+hipError_t launch_chunk_merge(const Plan& P, const ChunkRecs& R, float* weights, int* leaf_all, hipStream_t st);
+// mean[b,l,h] = dout . out32 over the head dim
+hipError_t launch_chunk_mean(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st);
+// dst (E, strides st3 (batch, row, head)) = src (float (B, R, H, D) contiguous)
+hipError_t launch_cast_rows(int dtype, const float* src, void* dst, const int64_t* st3, int64_t B, int64_t R,
+                            int64_t H, int64_t D, hipStream_t st);
 
 // leaf_gather.hip (leaf_block 1: the leaf stage is a value gather)
 hipError_t launch_gather_fwd(const Plan& P, const void* v, void* out, const char* rec, int bh0, int nbh,

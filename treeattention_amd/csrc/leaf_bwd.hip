@@ -27,8 +27,13 @@ struct LeafBwdArgs {
   float* delta;     // (B,L,H,S)
   void* dq_part;    // E (B,L,H,S,D)
   void* dv;         // E, v strides
-  float* dk_leaf;   // (B,L,H,D) or null
+  float* dk_leaf;   // (B,N,H,D) or null
+  float* dv32;      // chunked problem: dv as float (B,N,H,D) rows, else null
+  int first;        // chunked problem: the first chunk writes dv32 / dk_leaf, later ones add
 };
+
+// One element of the float accumulators of a chunked problem (or of dk_leaf).
+__device__ __forceinline__ void acc1f(float* p, float x, int first) { *p = first ? x : *p + x; }
 
 template <typename E>
 __device__ __forceinline__ void mov8(E* o, const E* p) {
@@ -266,8 +271,10 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
       if (key < LB) {
         const int64_t tok = (int64_t)beta * LB + key;
         const int d = 16 * nd + col;
-        dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[t][r];
-        if (a.dk_leaf) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = dkacc[t][r] * a.scale;
+        const int64_t th = (((int64_t)bb * a.N + tok) * a.H + h) * D + d;
+        if (a.dv32) acc1f(a.dv32 + th, dvacc[t][r], a.first);
+        else dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)dvacc[t][r];
+        if (a.dk_leaf) acc1f(a.dk_leaf + th, dkacc[t][r] * a.scale, a.first);
       }
     }
   }
@@ -563,7 +570,9 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kern
         if (key < LB) {
           const int64_t tok = (int64_t)beta * LB + key;
           const int d = 16 * (ndb + y) + col;
-          if (dkw) a.dk_leaf[(((int64_t)bb * a.N + tok) * a.H + h) * D + d] = acc[x][y][r] * a.scale;
+          const int64_t th = (((int64_t)bb * a.N + tok) * a.H + h) * D + d;
+          if (dkw) acc1f(a.dk_leaf + th, acc[x][y][r] * a.scale, a.first);
+          else if (a.dv32) acc1f(a.dv32 + th, acc[x][y][r], a.first);
           else dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)acc[x][y][r];
         }
       }
@@ -624,7 +633,9 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.delta = (float*)(ws + P.bws.delta);
   a.dq_part = ws + P.bws.dq_part;
   a.dv = dv;
-  a.dk_leaf = nodekeys ? nullptr : (float*)(ws + P.bws.dk_leaf);
+  a.dk_leaf = nodekeys ? nullptr : P.acc.dk_leaf ? P.acc.dk_leaf : (float*)(ws + P.bws.dk_leaf);
+  a.dv32 = P.acc.dv32;
+  a.first = P.acc.dv32 ? P.acc.first : 1;  // one launch: plain writes
   const unsigned grid = xcd_grid(P.BH, P.geo.NL);
   constexpr int smem8 = BwdTrTile<D, LBP>::bytes;
   if constexpr (sizeof(E) == 2 && LBP >= 32 && smem8 <= 160 * 1024) {

@@ -314,11 +314,14 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
 
 // out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows,
 // for the L * nbh queries of the launch's (batch, head) group, position-major
-// (consecutive threads write consecutive heads of one position).
+// (consecutive threads write consecutive heads of one position).  With out32
+// (a chunk of a problem with many samples) the sum goes to the float
+// (B, L, H, D) rows instead: written by the first chunk, added by later ones.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
                                                       E* __restrict__ out, int L, int H, int S, int bh0, int nbh,
-                                                      int64_t osb, int64_t osl, int64_t osh) {
+                                                      int64_t osb, int64_t osl, int64_t osh, float* __restrict__ out32,
+                                                      int first) {
   constexpr int TPQ = D / 8;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gid / TPQ;
@@ -329,6 +332,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ part
   const int64_t qh = (bb * L + l) * H + h;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   sum_rows8(acc, partial + (bhl * L + l) * S * D + 8 * part, D, slot_count[qh]);
+  if (out32) {
+    acc8f(out32 + qh * D + 8 * part, acc, first);
+    return;
+  }
   E* o = out + bb * osb + l * osl + h * osh + 8 * part;
   if constexpr (sizeof(E) == 2) {
     typedef __attribute__((ext_vector_type(8))) E e8;
@@ -406,7 +413,8 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   const int64_t nthr = nrows * (D / 8);
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
                      (const E*)a.partial, (const int*)(rec + P.rec.slot_count), (E*)out, (int)P.L, (int)P.H,
-                     (int)P.S, bh0, nbh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2]);
+                     (int)P.S, bh0, nbh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2], P.acc.out32,
+                     P.acc.first);
   return hipGetLastError();
 }
 

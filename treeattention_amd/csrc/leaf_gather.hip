@@ -51,6 +51,8 @@ struct GatherArgs {
   const int* order;
   const int* block_start;
   float* delta;
+  float* acc32;   // chunked problem: float (B, L|N, H, D) rows, written (first) or added to
+  int first;
 };
 
 // out[b, l, h, :] = sum over the query's distinct leaves (slot order) of
@@ -82,7 +84,8 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs a, int bh0, 
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] += w[j] * x[j][i];
   }
-  store8f((E*)a.out + bb * a.osb + l * a.osl + h * a.osh + d0, acc);
+  if (a.acc32) acc8f(a.acc32 + qh * a.D + d0, acc, a.first);
+  else store8f((E*)a.out + bb * a.osb + l * a.osl + h * a.osh + d0, acc);
 }
 
 // dv[b, n, h, :] = sum over leaf n's bucket (query order) of W_u dout_l, and
@@ -131,7 +134,10 @@ __global__ __launch_bounds__(256) void scatter_dv_kernel(GatherArgs a) {
       if (d0 == 0 && e + j < e1) a.delta[slot[j]] = dot;
     }
   }
-  if (on) store8f((E*)a.out + bb * a.osb + n * a.osl + h * a.osh + d0, acc);
+  if (on) {
+    if (a.acc32) acc8f(a.acc32 + ((bb * (int64_t)a.N + n) * a.H + h) * a.D + d0, acc, a.first);
+    else store8f((E*)a.out + bb * a.osb + n * a.osl + h * a.osh + d0, acc);
+  }
 }
 
 static GatherArgs gather_args(const Plan& P, const void* v, const char* rec) {
@@ -153,6 +159,8 @@ static GatherArgs gather_args(const Plan& P, const void* v, const char* rec) {
   a.order = (const int*)(rec + P.rec.order);
   a.block_start = (const int*)(rec + P.rec.block_start);
   a.delta = nullptr;
+  a.acc32 = nullptr;
+  a.first = P.acc.first;
   return a;
 }
 
@@ -162,6 +170,7 @@ static hipError_t gather_fwd_t(const Plan& P, const void* v, void* out, const ch
   GatherArgs a = gather_args(P, v, rec);
   a.out = out;
   a.osb = P.p.o_strides[0]; a.osl = P.p.o_strides[1]; a.osh = P.p.o_strides[2];
+  a.acc32 = P.acc.out32;
   const int64_t nrows = (int64_t)nbh * P.L;
   const int64_t nthr = nrows * (P.D / 8);
   hipLaunchKernelGGL(gather_fwd_kernel<E>, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st, a, bh0, nrows);
@@ -177,6 +186,7 @@ static hipError_t gather_bwd_t(const Plan& P, const void* v, const void* g, void
   a.delta = delta;
   a.out = dv;
   a.osb = P.p.v_strides[0]; a.osl = P.p.v_strides[1]; a.osh = P.p.v_strides[2];
+  a.acc32 = P.acc.dv32;
   const int tp = P.D <= 32 ? 4 : P.D <= 64 ? 8 : 16;
   const int64_t nthr = P.N * tp;
   const dim3 grid((unsigned)((nthr + 255) / 256), (unsigned)P.BH);

@@ -30,6 +30,7 @@ namespace ta {
 struct SampleArgs {
   Geo geo;
   int B, L, H, S, causal, coff;  // coff = N - L: causal offset of query positions
+  int s0, stot;   // this launch's samples are s0 .. s0 + S - 1 of stot (uniform and path indexing)
   float maxhalf;
   const void* q;
   int64_t qsb, qsl, qsh;
@@ -44,6 +45,7 @@ struct SampleArgs {
   int* slot_leaf;
   float* slot_weight;
   int* slot_count;
+  float* lse;            // (B, L, H): log of the sum over the query's samples of exp(log-prob)
   const uint8_t* paths;  // replay: packed path bits (L, B, H, S, nbytes), else null
   int nbits, nbytes;
   int Td;         // depths d >= Td are sparse: per-item child logits instead of level tiles
@@ -270,10 +272,11 @@ struct Walk {
       if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
       const int l = l0 + min(iq[k], nq - 1);
       iblk[k] = (l + a.coff) / G.LB;
-      ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * S + is[k]) * T) * b;
+      ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * a.stot + a.s0 + is[k]) * T) * b;
       rleaf[k] = 0u;
       if (kReplay && iq[k] < kQueryTile)
-        rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * S + is[k]) * a.nbytes, a.nbits, a.nbytes);
+        rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * a.stot + a.s0 + is[k]) * a.nbytes,
+                             a.nbits, a.nbytes);
     }
 #pragma unroll
     for (int k = 0; k < kNC; ++k) {
@@ -472,7 +475,8 @@ struct Walk {
       for (int k = 0; k < kNI; ++k) {
         const float m = row_max16(acc[k]);
         const float e = fast_exp2((acc[k] - m) * kLog2e);
-        const float inv = 1.f / row_sum16(e);
+        const float se = row_sum16(e);
+        const float inv = 1.f / se;
         float tot = e;  // weight of this leaf block summed over the samples from s on
         bool fst = true;
         row_dups16(node[k], e, s, tot, fst);
@@ -488,7 +492,10 @@ struct Walk {
           a.slot_leaf[qh * S + rank] = node[k];
           a.slot_weight[qh * S + rank] = tot * inv;
         }
-        if (s == 0) a.slot_count[qh] = cnt;
+        if (s == 0) {
+          a.slot_count[qh] = cnt;
+          a.lse[qh] = m + fast_log2(se) * kLn2;
+        }
       }
       return;
     }
@@ -525,6 +532,7 @@ struct Walk {
         }
       }
       const float inv = 1.f / sum;
+      if (s == 0) a.lse[(((int64_t)bb * a.L + l0 + qi) * a.H + h)] = m + fast_log2(sum) * kLn2;
       wgt[k] = fast_exp2((acc[k] - m) * kLog2e) * inv;
       first[k] = fst;
       acc[k] = tot * inv;  // summed weight of this leaf block (used if first)
@@ -844,6 +852,8 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.L = (int)P.L;
   a.H = (int)P.H;
   a.S = (int)P.S;
+  a.s0 = (int)P.s0;
+  a.stot = (int)P.s_total;
   a.causal = P.p.causal == TA_CAUSAL_EXACT;
   a.coff = (int)(P.N - P.L);
   a.maxhalf = 0.5f * P.p.max_logit;
@@ -864,6 +874,7 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.slot_leaf = (int*)(rec + P.rec.slot_leaf);
   a.slot_weight = (float*)(rec + P.rec.slot_weight);
   a.slot_count = (int*)(rec + P.rec.slot_count);
+  a.lse = (float*)(rec + P.rec.lse);
   a.Td = P.sample_dense;
   a.pair_rows = P.p.tree_mode != TA_TREE_NATURAL && P.geo.b == 2;
   a.logA = (float*)(rec + P.rec.logA);

@@ -71,6 +71,10 @@ struct TreeArgs {
   int Tb, nsd;
   int dqp;  // 1: add each query's per-pair dq rows (leaf dq and deep-level tree dq)
   int dkl;  // 1: add the leaf part of dk
+  // a chunk of a problem with many samples: dq goes to float rows (written by
+  // the first chunk, added by later ones), and so does the summary gradient
+  float* dq32;
+  int first;
 };
 
 template <typename E>
@@ -96,10 +100,12 @@ __device__ __forceinline__ float clamp_h(float x, float m) { return fminf(fmaxf(
 
 // dl_u = W_u (delta_u - sum_u' W_u' delta_u').  Lane group of P lanes (P =
 // S rounded up to a power of two) per (b, l, h); butterfly sum in the group.
+// A chunk of a problem with many samples passes the sum over all its samples
+// (dout . out) as `mean` (its W are the weights over all samples).
 __global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__ slot_count,
                                                          const float* __restrict__ slot_weight,
                                                          const float* __restrict__ delta, float* __restrict__ dl,
-                                                         int S, int P, int64_t nqh) {
+                                                         int S, int P, int64_t nqh, const float* __restrict__ mean) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t qh = gid / P;
   const int u = (int)(gid - qh * P);
@@ -109,7 +115,11 @@ __global__ __launch_bounds__(256) void slot_dlogp_kernel(const int* __restrict__
   const float w = act ? slot_weight[qh * S + u] : 0.f;
   const float dt = act ? delta[qh * S + u] : 0.f;
   float tot = w * dt;
-  for (int o = 1; o < P; o <<= 1) tot += __shfl_xor(tot, o, 64);
+  if (mean) {
+    tot = in ? mean[qh] : 0.f;
+  } else {
+    for (int o = 1; o < P; o <<= 1) tot += __shfl_xor(tot, o, 64);
+  }
   if (act) dl[qh * S + u] = w * (dt - tot);
 }
 
@@ -729,6 +739,10 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
         acc[4] += 2.f * gv * x1.x; acc[5] += 2.f * gv * x1.y; acc[6] += 2.f * gv * x1.z; acc[7] += 2.f * gv * x1.w;
       }
     }
+    if (a.dq32) {
+      acc8f(a.dq32 + qh * D + d0, acc, a.first);
+      continue;
+    }
     E* o = dq + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh + d0;
     if constexpr (sizeof(E) == 2) {
       typedef __attribute__((ext_vector_type(8))) E e8;
@@ -899,7 +913,7 @@ __global__ __launch_bounds__(512) void tree_dc_kernel(TreeArgs a) {
 // dsum rows of the dense levels (the first nsd rows of each (batch, head)) =
 // sum over query splits (in split order); rows outside any level are 0.
 __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restrict__ part, float* __restrict__ dsum,
-                                                          int64_t n, int qsplit, Geo G, int D, int nsd) {
+                                                          int64_t n, int qsplit, Geo G, int D, int nsd, int first) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= n) return;
   const int64_t row = e / D, bh = row / nsd, r = row - bh * nsd;
@@ -908,7 +922,8 @@ __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restric
   float s = 0.f;
   if (r - G.off[lam] < G.pw[lam])
     for (int k = 0; k < qsplit; ++k) s += part[(int64_t)k * n + e];
-  dsum[(bh * G.NS + r) * D + (e - row * D)] = s;
+  float* o = dsum + (bh * G.NS + r) * D + (e - row * D);
+  *o = first ? s : *o + s;
 }
 
 // dk[b, t, h, :] = dk_leaf + sum over the summaries that include token t.
@@ -1029,6 +1044,7 @@ struct BandArgs {
   const int* block_start;
   void* dq_part;
   float* dsum;
+  int first;  // 0: add to the summary-gradient rows (a later chunk of a problem with many samples)
 };
 
 constexpr int kBandRows = 64;  // dC rows of one band's subtree (b = 2: 5 depths, b = 4: 2)
@@ -1249,7 +1265,8 @@ __global__ __launch_bounds__(256, 2) void tree_band_kernel(BandArgs a) {
         ++j;
       }
       const int64_t grow = G.off[da + j + 1] + ((int64_t)s0 << (lb * (j + 1))) + lr;
-      a.dsum[((int64_t)bh * G.NS + grow) * D + 16 * ct + col] = acc[k][r];
+      float* o = a.dsum + ((int64_t)bh * G.NS + grow) * D + 16 * ct + col;
+      *o = a.first ? acc[k][r] : *o + acc[k][r];
     }
   }
 }
@@ -1324,8 +1341,11 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.Lp = P.Lp;
   a.dq = dq;
   a.dsum_part = (float*)(ws + P.bws.dsum_part);
-  a.dsum = (float*)(ws + P.bws.dsum);
-  a.dk_leaf = (const float*)(ws + P.bws.dk_leaf);
+  const bool chunk = P.acc.dq32 != nullptr;  // a chunk of a problem with many samples
+  a.dsum = chunk ? P.acc.dsum : (float*)(ws + P.bws.dsum);
+  a.dk_leaf = chunk ? P.acc.dk_leaf : (const float*)(ws + P.bws.dk_leaf);
+  a.dq32 = P.acc.dq32;
+  a.first = chunk ? P.acc.first : 1;
   a.dk = dk;
   a.ksb = P.p.k_strides[0]; a.ksl = P.p.k_strides[1]; a.ksh = P.p.k_strides[2];
   a.qsplit = P.qsplit;
@@ -1347,7 +1367,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   int pw2 = 1;
   while (pw2 < P.S) pw2 <<= 1;
   hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
-                     a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh);
+                     a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh, P.acc.mean);
   if (a.refc)
     hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
   // the band depths (before tree_dq_kernel, whose epilogue sums the pairs' dq rows)
@@ -1370,6 +1390,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     ba.block_start = (const int*)(rec + P.rec.block_start);
     ba.dq_part = ws + P.bws.dq_part;
     ba.dsum = a.dsum;
+    ba.first = a.first;
     for (int da = P.tree_dense; da < P.geo.T; da += nbmax) {
       ba.da = da;
       ba.nb = P.geo.T - da < nbmax ? P.geo.T - da : nbmax;
@@ -1408,8 +1429,9 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     hipLaunchKernelGGL((tree_dc_kernel<E, D>), dim3(chunks, P.qsplit, P.BH), dim3(512), 0, st, a);
     const int64_t n = P.BH * (int64_t)a.nsd * D;
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D, a.nsd);
+                       (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D, a.nsd, a.first);
   }
+  if (chunk && !P.acc.last) return hipGetLastError();  // the key adjoint runs once, after the last chunk
   if (P.p.tree_mode == TA_TREE_NODEKEYS) {
     const int64_t n = (int64_t)(P.geo.NL - 1) * D;
     if (n > 0)

@@ -30,7 +30,8 @@ _DTYPES = {torch.float32: _lib.TA_F32, torch.bfloat16: _lib.TA_BF16, torch.float
 class TreeOptions:
     """How the tree is built and sampled.
 
-    * ``num_samples``: paths per query (1..64).
+    * ``num_samples``: paths per query (1..1024; above 64 in chunks of at most 64,
+      non-causal or exact causal).
     * ``branching``, ``leaf_block``: ``N = leaf_block * branching**T``.
     * ``tree_mode``: ``"compat"`` (reference key layout: in-order Haar of the
       leaf-block means, read in heap order), ``"natural"`` (child summary =
