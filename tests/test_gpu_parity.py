@@ -272,6 +272,35 @@ def test_seed_path_equals_explicit_uniforms_and_is_deterministic():
         assert torch.equal(a, c)
 
 
+@pytest.mark.parametrize("view", ["head_slice", "fused_qkv"])
+def test_strided_views_with_gaps(view):
+    """q / k / v as views with gaps between rows (a slice of the heads, or q, k, v inside one
+    fused (B, L, 3, H, D) tensor): the same results, bit for bit, as contiguous copies, with the
+    gradients in buffers of the views' shapes."""
+    from treeattention_amd.function import TreeOptions, tree_backward, tree_forward
+
+    B, L, H, D, S, b, LB = 1, 512, 4, 64, 8, 2, 16
+    print(f"[case] strided views {view}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    if view == "head_slice":
+        big = [torch.randn(B, L, 2 * H, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3)]
+        q, k, v = (t[:, :, H:] for t in big)
+    else:
+        qkv = torch.randn(B, L, 3, H, D, device="cuda", generator=g).to(torch.bfloat16)
+        q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    do = torch.randn(B, L, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    opts = TreeOptions(num_samples=S, branching=b, leaf_block=LB, tree_mode="natural", causal=True, seed=4)
+    o1, w1, r1 = tree_forward(q, k, v, opts)
+    grads1 = tree_backward(q, k, v, w1, r1, do, opts)
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    o2, w2, r2 = tree_forward(qc, kc, vc, opts)
+    grads2 = tree_backward(qc, kc, vc, w2, r2, do, opts)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(w1, w2)
+    for a, c in zip(grads1, grads2):
+        assert a.shape == c.shape and torch.equal(a, c)
+
+
 # (L, B, H, D, S) of the reference's own end-to-end parity test
 # (test_harness_smoke.py:824-917); D = 16 runs zero-padded to 32 head dims.
 REFERENCE_E2E_SHAPES = [(8, 1, 2, 16, 4), (32, 2, 2, 16, 4), (64, 1, 8, 16, 4), (128, 1, 2, 64, 8), (512, 2, 4, 32, 8),

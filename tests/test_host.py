@@ -64,6 +64,22 @@ def test_float_leaf_tiles_fit(D, LB):
     _lib.byte_sizes(_problem(dtype=_lib.TA_F32, D=D, leaf_block=LB, N=N, L=N, branching=2, causal=0))
 
 
+def test_backward_inputs_without_gaps():
+    """dq / dk / dv are written with the strides of q / k / v into ``empty_like`` buffers, so
+    the backward takes views with gaps (a slice of heads, q inside a fused qkv tensor) as
+    contiguous copies and dense layouts (any dim order) as they are."""
+    from treeattention_amd.function import _dense
+
+    x = torch.randn(2, 64, 16, 32)
+    assert _dense(x) is x
+    p = x.permute(1, 0, 2, 3)
+    assert _dense(p) is p and torch.empty_like(p).stride() == p.stride()
+    for view in (x[:, :, 4:8], torch.randn(2, 64, 3, 16, 32)[:, :, 0], x[:, ::2]):
+        d = _dense(view)
+        assert d.is_contiguous() and torch.equal(d, view)
+        assert torch.empty_like(d).stride() == d.stride()
+
+
 def test_many_samples_run_in_chunks():
     """More than 64 samples: the record holds one chunk record per <= 64 samples plus every
     sample's leaf block and the float output; workspaces are reused chunk after chunk."""

@@ -91,6 +91,20 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _dense(t: torch.Tensor) -> torch.Tensor:
+    """``t`` if its elements fill its span without gaps (any dim order), else a contiguous
+    copy.  The backward writes dq / dk / dv with the strides of q / k / v into buffers from
+    ``torch.empty_like``, which keeps the strides of dense tensors only: a view with gaps
+    (a slice of heads, one of q / k / v inside a fused qkv tensor) would send the writes past
+    the gradient's end."""
+    expect = 1
+    for st, n in sorted((st, n) for st, n in zip(t.stride(), t.shape) if n > 1):
+        if st != expect:
+            return t.contiguous()
+        expect *= n
+    return t
+
+
 _HEAD_DIMS = (32, 64, 96, 128)
 
 
@@ -231,7 +245,7 @@ def tree_backward(q, k, v, weights, record, grad_out, opts: TreeOptions):
         grad_out = torch.nn.functional.pad(grad_out, (0, q.shape[-1] - D))
         dq, dk, dv = tree_backward(q, k, v, weights, record, grad_out, opts)
         return dq[..., :D], dk[..., :D], dv[..., :D]
-    q, k, v = _prep(q), _prep(k), _prep(v)
+    q, k, v = _dense(_prep(q)), _dense(_prep(k)), _dense(_prep(v))
     grad_out = _prep(grad_out)
     prob = make_problem(q, k, v, opts)
     prob.g_strides[:] = _strides(grad_out, opts.layout)
