@@ -19,7 +19,6 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 constexpr int kMaxDepth = 24;     // b^T = NL leaf blocks; b >= 2 so T <= 24 covers NL <= 2^24
 constexpr int kMaxSamples = 64;   // one wavefront lane per sample
 constexpr int kQueryTile = 64;    // queries per workgroup in the tree kernels
-constexpr int kChunk = 128;       // child-summary columns per MFMA logit chunk
 constexpr int kSampleDenseCols = 1024;  // widest level the sampler evaluates as level tiles
 constexpr int kTreeDenseCols = 1024;    // widest level the backward's dense G tiles cover
 constexpr int kDetMaxLeaves = TA_DET_MAX_LEAVES;  // deterministic mode: leaves per row held in LDS

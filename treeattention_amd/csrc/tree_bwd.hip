@@ -30,8 +30,12 @@
 
 namespace ta {
 
-constexpr int kXS = kChunk + 4;       // padded row stride (floats) of the logit tile
-constexpr int kGS = kChunk + 8;       // padded row stride (elements) of G[q][col]
+// Child-summary columns per MFMA logit chunk of tree_dq_kernel: 64 at head
+// dims up to 64 (the query tile's LDS then leaves room for three workgroups
+// per CU; measured 19 % faster at D = 32 and 64), 128 above (where the
+// registers allow two workgroups per CU either way and more chunks cost more
+// barriers).  The logit tile's row stride is CH + 4 floats, G's CH + 8 elements.
+constexpr int chunk_cols(int D) { return D <= 64 ? 64 : 128; }
 
 struct TreeArgs {
   Geo geo;
@@ -199,13 +203,13 @@ __global__ __launch_bounds__(256) void ref_causal_grad_kernel(TreeArgs a) {
 // the chunk, and each query's distinct leaf blocks, their dl and count.
 template <typename E>
 struct TileSmem {
-  float* Xs;   // [64][kXS]
-  E* Gm;       // [64][kGS]
+  float* Xs;   // [64][chunk columns + 4]
+  E* Gm;       // [64][chunk columns + 8]
   int* lf;     // [64][S]
   float* dls;  // [64][S]
   int* cn;     // [64]
-  float* scv;  // [64 * 16][2] per scan lane of a level: A_row, A_n (S <= 16)
-  int* sci;    // [64 * 16][3] per scan lane: child row, node, run-end flags | children mask << 8
+  float* scv;  // [64 * P][2] per scan lane of a level: A_row, A_n (P = 8 or 16 lanes per query)
+  int* sci;    // [64 * P][3] per scan lane: child row, node, run-end flags | children mask << 8
 };
 
 template <typename E>
@@ -306,7 +310,7 @@ __device__ __forceinline__ void build_g_scan(const Geo& G, int d, int S, int nq,
   }
 }
 
-template <typename E, int P, int kB>
+template <typename E, int P, int kB, int kXS, int kGS>
 __device__ __forceinline__ void build_g_emit(const Geo& G, int c0, int ncols, float maxhalf, const float* Xs,
                                              const float* scv, const int* sci, E* Gm, int tid) {
   constexpr int LP = P <= 1 ? 0 : P <= 2 ? 1 : P <= 4 ? 2 : P <= 8 ? 3 : 4;
@@ -363,7 +367,7 @@ __device__ __forceinline__ void build_g_emit(const Geo& G, int c0, int ncols, fl
 // writer and every sum a fixed order: deterministic, no atomics.  Clamped
 // logits get 0.
 // kB: the branching factor when known at compile time (2 or 4), else 0.
-template <typename E, int P, int kB>
+template <typename E, int P, int kB, int kXS, int kGS>
 __device__ __forceinline__ void build_g_p(const Geo& G, int d, int c0, int ncols, int S, int nq, float maxhalf,
                                           const float* Xs, const int* lf, const float* dls, const int* cn, E* Gm,
                                           int tid) {
@@ -492,6 +496,8 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   using F = typename M::frag;
   constexpr int KS = D / M::K;
   constexpr int NMD = (D / 16 + 3) / 4;  // head-dim tiles per wave
+  constexpr int kChunk = chunk_cols(D), kXS = kChunk + 4, kGS = kChunk + 8;
+  constexpr int kSL = kP <= 8 ? 8 : 16;  // hoisted scan lanes per query
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
@@ -508,7 +514,7 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
   sm.dls = (float*)(sm.lf + kQueryTile * S);
   sm.cn = (int*)(sm.dls + kQueryTile * S);
   sm.scv = (float*)(sm.cn + kQueryTile);
-  sm.sci = (int*)(sm.scv + 2 * kQueryTile * 16);
+  sm.sci = (int*)(sm.scv + 2 * kQueryTile * kSL);
 
   RowFrags<E, D> qa[4];
 #pragma unroll
@@ -644,12 +650,13 @@ __global__ __launch_bounds__(256, 2) void tree_dq_kernel(TreeArgs a) {
     if constexpr (kP <= 16 && (kB == 2 || kB == 4)) {
       if (lvl > kChunk) {  // the level's scans once, at its first chunk
         if (c0 == 0) build_g_scan<E, kP, kB>(G, d, S, nq, sm.lf, sm.dls, sm.cn, sm.scv, sm.sci, tid);
-        if (rcols > 0) build_g_emit<E, kP, kB>(G, c0, rcols, a.maxhalf, sm.Xs, sm.scv, sm.sci, sm.Gm, tid);
+        if (rcols > 0)
+          build_g_emit<E, kP, kB, kXS, kGS>(G, c0, rcols, a.maxhalf, sm.Xs, sm.scv, sm.sci, sm.Gm, tid);
       } else if (rcols > 0) {
-        build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+        build_g_p<E, kP, kB, kXS, kGS>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
       }
     } else if (rcols > 0) {
-      build_g_p<E, kP, kB>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
+      build_g_p<E, kP, kB, kXS, kGS>(G, d, c0, rcols, S, nq, a.maxhalf, sm.Xs, sm.lf, sm.dls, sm.cn, sm.Gm, tid);
     }
     __syncthreads();
     if (a.refc) {
@@ -1309,8 +1316,9 @@ __global__ __launch_bounds__(256) void ref_band_boundary_kernel(TreeArgs a, int 
 static int tree_smem(const Plan& P) {
   const int S = (int)P.S;
   // + the hoisted scan lanes (S <= 16): two floats and three ints each
-  return kQueryTile * kXS * 4 + kQueryTile * kGS * P.esize + kQueryTile * S * 8 + kQueryTile * 4 +
-         (S <= 16 ? kQueryTile * 16 * 20 : 0);
+  const int ch = chunk_cols((int)P.D);
+  return kQueryTile * (ch + 4) * 4 + kQueryTile * (ch + 8) * P.esize + kQueryTile * S * 8 + kQueryTile * 4 +
+         (S <= 8 ? kQueryTile * 8 * 20 : S <= 16 ? kQueryTile * 16 * 20 : 0);
 }
 
 template <typename E, int D>
