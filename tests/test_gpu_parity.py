@@ -194,11 +194,22 @@ def test_levels_wider_than_one_sampler_pass(b, L, LB, causal):
 
 
 @pytest.mark.parametrize("S,b,LB,L,D,causal,dtype", [(32, 4, 16, 1024, 64, True, torch.bfloat16),
-                                                     (64, 2, 8, 512, 32, False, torch.float32)])
+                                                     (64, 2, 8, 512, 32, False, torch.float32),
+                                                     (24, 2, 4, 1024, 128, True, torch.bfloat16),
+                                                     (48, 4, 16, 1024, 64, False, torch.float16),
+                                                     (20, 8, 8, 512, 32, True, torch.float32),
+                                                     (40, 8, 1, 512, 32, False, torch.bfloat16)])
 def test_more_than_sixteen_samples(S, b, LB, L, D, causal, dtype):
-    # 16 (query, sample) items per sampler thread and 64-lane groups per query
-    # in the tree-gradient scans
+    # 8 (S <= 32) or 16 (query, sample) items per sampler thread and 32- or
+    # 64-lane groups per query in the tree-gradient scans, branching 2 and 4
+    # specialized, 8 generic
     run_case(1, L, 2, D, S, b, LB, "natural", causal, dtype)
+
+
+@pytest.mark.parametrize("S", [24, 64])
+def test_more_than_sixteen_samples_reference_tree(S):
+    # the reference's default of 64 paths on its own tree, per-path levels forced on
+    run_case(1, 1024, 2, 64, S, 2, 1, "compat", False, torch.bfloat16, dense_cols=64)
 
 
 @pytest.mark.parametrize("b,LB,L,causal", [(8, 1, 512, False), (16, 16, 4096, True)])

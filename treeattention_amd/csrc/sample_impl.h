@@ -206,6 +206,20 @@ __device__ __forceinline__ void row_dups16(int n, float e, int s, float& tot, bo
     row_dups16<R + 1>(n, e, s, tot, fst);
   }
 }
+// x from lane j ^ M of this 16-lane row (M = 1, 2, 4, 8), by DPP moves:
+// quad_perm [1, 0, 3, 2] for M = 1, a rotation by 8 for M = 8, else the
+// rotation by M or by 16 - M, whichever lands on j ^ M.
+template <int M>
+__device__ __forceinline__ float row_xor(float x, int j) {
+  if constexpr (M == 1) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+  } else if constexpr (M == 8) {
+    return row_ror<8>(x);
+  } else {
+    const float dn = row_ror<M>(x), up = row_ror<16 - M>(x);
+    return (j & M) ? dn : up;
+  }
+}
 // Lane j of each 16-lane row holds p[m] = its part of item m's sum (m < 16);
 // returns item j's total (sum over the row's lanes of p[j]), by halving
 // exchanges with lanes j ^ 8, j ^ 4, j ^ 2, j ^ 1.
@@ -214,20 +228,20 @@ __device__ __forceinline__ float row_reduce_scatter16(const float (&p)[16], int 
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const bool up = j & 8;
-    v8[i] = (up ? p[i + 8] : p[i]) + __shfl_xor(up ? p[i] : p[i + 8], 8, 64);
+    v8[i] = (up ? p[i + 8] : p[i]) + row_xor<8>(up ? p[i] : p[i + 8], j);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool up = j & 4;
-    v4[i] = (up ? v8[i + 4] : v8[i]) + __shfl_xor(up ? v8[i] : v8[i + 4], 4, 64);
+    v4[i] = (up ? v8[i + 4] : v8[i]) + row_xor<4>(up ? v8[i] : v8[i + 4], j);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const bool up = j & 2;
-    v2[i] = (up ? v4[i + 2] : v4[i]) + __shfl_xor(up ? v4[i] : v4[i + 2], 2, 64);
+    v2[i] = (up ? v4[i + 2] : v4[i]) + row_xor<2>(up ? v4[i] : v4[i + 2], j);
   }
   const bool up = j & 1;
-  return (up ? v2[1] : v2[0]) + __shfl_xor(up ? v2[0] : v2[1], 1, 64);
+  return (up ? v2[1] : v2[0]) + row_xor<1>(up ? v2[0] : v2[1], j);
 }
 
 // rank = number of row keys below n; cnt = number of row keys that are not
@@ -250,39 +264,47 @@ __device__ __forceinline__ void row_rank16(int key, int n, int& rank, int& cnt) 
 // and the sparse-level kernel share both.
 template <int kB, int kNI, bool kReplay>
 struct Walk {
-  static constexpr int kNC = kB == 2 ? kNI : 1;  // b = 2: two decisions share a Philox block
-  int node[kNI], iq[kNI], is[kNI], iblk[kNI];
-  uint32_t rleaf[kNI];  // replay: the given leaf block of each item
-  int64_t ubase[kNI];
+  // Per item: its node, (query << 8) | sample (query kQueryTile: inactive),
+  // causal boundary leaf block, log-prob and, for b = 2 (two decisions per
+  // Philox block), the block's last two words with the block's counter as
+  // the tag: entered at word 0, a block serves the next decision from there.
+  // The uniforms' index is recomputed from ub0 (the tile's first query and
+  // sample) per decision, so few registers hold an item.
+  static constexpr int kNC = kB == 2 ? kNI : 1;
+  int node[kNI], qs[kNI], iblk[kNI];
+  uint32_t rleaf[kReplay ? kNI : 1];  // replay: the given leaf block of each item
   float acc[kNI];
-  RngCache rc[kNC];
+  uint32_t rtag[kNC], rw2[kNC], rw3[kNC];
+  int64_t ub0;  // uniforms' (b, l, h, s) row of the tile's first query, sample 0
+
+  __device__ __forceinline__ int iq(int k) const { return qs[k] >> 8; }
+  __device__ __forceinline__ int is(int k) const { return qs[k] & 255; }
 
   __device__ __forceinline__ void init(const SampleArgs& a, int l0, int nq, int bb, int h, int tid) {
     const Geo& G = a.geo;
-    const int S = a.S, T = G.T;
-    const int b = kB ? kB : G.b;
+    const int S = a.S;
     const int nitems = kQueryTile * S;
+    ub0 = (((int64_t)bb * a.L + l0) * a.H + h) * a.stot + a.s0;
 #pragma unroll
     for (int k = 0; k < kNI; ++k) {
       const int it = tid + 256 * k;
       node[k] = 0;
       acc[k] = 0.f;
-      iq[k] = it < nitems ? it / S : kQueryTile;
-      is[k] = it < nitems ? it - iq[k] * S : 0;
-      if (iq[k] >= nq) iq[k] = kQueryTile;  // inactive item
-      const int l = l0 + min(iq[k], nq - 1);
+      int q = it < nitems ? it / S : kQueryTile;
+      const int sm = it < nitems ? it - q * S : 0;
+      if (q >= nq) q = kQueryTile;  // inactive item
+      qs[k] = (q << 8) | sm;
+      const int l = l0 + min(q, nq - 1);
       iblk[k] = (l + a.coff) / G.LB;
-      ubase[k] = (((((int64_t)bb * a.L + l) * a.H + h) * a.stot + a.s0 + is[k]) * T) * b;
-      rleaf[k] = 0u;
-      if (kReplay && iq[k] < kQueryTile)
-        rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * a.stot + a.s0 + is[k]) * a.nbytes,
-                             a.nbits, a.nbytes);
+      if constexpr (kReplay) {
+        rleaf[k] = 0u;
+        if (q < kQueryTile)
+          rleaf[k] = path_leaf(a.paths + ((((int64_t)l * a.B + bb) * a.H + h) * a.stot + a.s0 + sm) * a.nbytes,
+                               a.nbits, a.nbytes);
+      }
     }
 #pragma unroll
-    for (int k = 0; k < kNC; ++k) {
-      rc[k].ctr = ~0ull;
-      rc[k].w0 = rc[k].w1 = rc[k].w2 = rc[k].w3 = 0u;
-    }
+    for (int k = 0; k < kNC; ++k) rtag[k] = rw2[k] = rw3[k] = 0u;
   }
 
   // One decision of item k at depth d from its node's b child logits xr[0..b)
@@ -292,7 +314,7 @@ struct Walk {
     const Geo& G = a.geo;
     const int T = G.T, lb = G.lb;
     const int b = kB ? kB : G.b;
-    const int qi = iq[k];
+    const int qi = iq(k);
     const int shb = lb * (T - d), shc = lb * (T - 1 - d);
     // log-sum-exp of the clamped child logits
     float lse;
@@ -341,7 +363,8 @@ struct Walk {
       la_d = logA[qi * (T + 1) + d];
       la_c = logA[qi * (T + 1) + d + 1];
     }
-    const int64_t ub = ubase[k] + d * b;
+    // index of the decision's first uniform in (B, L, H, stot, T, b)
+    const int64_t ub = ((ub0 + (int64_t)qi * a.H * a.stot + is(k)) * T + d) * b;
     if constexpr (kB != 0) {
       // Gumbel-max in ratio form: lp_j - ln(-ln u_j) is, up to constants
       // common to all children, ln(p_j / E_j) with E_j = -log2 u_j > 0,
@@ -358,9 +381,27 @@ struct Walk {
 #pragma unroll
           for (int j = 0; j < 4; ++j) u[j] = word_to_uniform(ph.w[j]);
         }
-      } else {
-#pragma unroll
-        for (int j = 0; j < kB; ++j) u[j] = uniform_at(a.U, a.seed, ub + j, rc[kB == 2 ? k : 0]);
+      } else {  // b = 2: ub is even, so the decision takes words 0, 1 or 2, 3 of a block
+        if (a.U) {
+          u[0] = a.U[ub];
+          u[1] = a.U[ub + 1];
+        } else {
+          const uint64_t ctr = (uint64_t)ub >> 2;
+          const bool hi = ub & 2;
+          // rtag holds ctr + 1 of the block entered at word 0 (0: none), so a
+          // fresh item never matches
+          if (hi && rtag[k] == (uint32_t)ctr + 1u) {
+            u[0] = word_to_uniform(rw2[k]);
+            u[1] = word_to_uniform(rw3[k]);
+          } else {
+            const Philox4 ph = philox4x32_10(ctr, a.seed);
+            u[0] = word_to_uniform(hi ? ph.w[2] : ph.w[0]);
+            u[1] = word_to_uniform(hi ? ph.w[3] : ph.w[1]);
+            rtag[k] = hi ? 0u : (uint32_t)ctr + 1u;
+            rw2[k] = ph.w[2];
+            rw3[k] = ph.w[3];
+          }
+        }
       }
       float wj[kB];
 #pragma unroll
@@ -431,8 +472,8 @@ struct Walk {
     const int S = a.S, T1 = a.geo.T + 1;
 #pragma unroll
     for (int k = 0; k < kNI; ++k) {
-      if (iq[k] >= kQueryTile) continue;
-      const int64_t o = (((int64_t)bb * a.L + l0 + iq[k]) * a.H + h) * S + is[k];
+      if (iq(k) >= kQueryTile) continue;
+      const int64_t o = (((int64_t)bb * a.L + l0 + iq(k)) * a.H + h) * S + is(k);
       a.leaf[o] = node[k];
       a.slot_weight[o] = acc[k];
     }
@@ -446,8 +487,8 @@ struct Walk {
     const int S = a.S, T1 = a.geo.T + 1;
 #pragma unroll
     for (int k = 0; k < kNI; ++k) {
-      if (iq[k] >= kQueryTile) continue;
-      const int64_t o = (((int64_t)bb * a.L + l0 + iq[k]) * a.H + h) * S + is[k];
+      if (iq(k) >= kQueryTile) continue;
+      const int64_t o = (((int64_t)bb * a.L + l0 + iq(k)) * a.H + h) * S + is(k);
       node[k] = a.leaf[o];
       acc[k] = a.slot_weight[o];
     }
@@ -482,7 +523,7 @@ struct Walk {
         row_dups16(node[k], e, s, tot, fst);
         int rank = 0, cnt = 0;
         row_rank16(fst ? node[k] : 0x7fffffff, node[k], rank, cnt);
-        const int qi = iq[k];
+        const int qi = iq(k);
         if (qi >= kQueryTile) continue;
         const int l = l0 + qi;
         const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
@@ -514,9 +555,9 @@ struct Walk {
     for (int k = 0; k < kNI; ++k) {
       wgt[k] = 0.f;
       first[k] = false;
-      const int qi = iq[k];
+      const int qi = iq(k);
       if (qi >= kQueryTile) continue;
-      const int s = is[k];
+      const int s = is(k);
       const int* lq = lf + qi * S;
       const float* pq = lps + qi * S;
       float m = -__builtin_inff();
@@ -541,15 +582,15 @@ struct Walk {
   #pragma unroll
     for (int k = 0; k < kNI; ++k) {
       const int it = tid + 256 * k;
-      if (iq[k] < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
+      if (iq(k) < kQueryTile) fl[it] = first[k] ? node[k] : 0x7fffffff;
       else if (it < nitems) fl[it] = 0x7fffffff;
     }
     __syncthreads();
   #pragma unroll
     for (int k = 0; k < kNI; ++k) {
-      const int qi = iq[k];
+      const int qi = iq(k);
       if (qi >= kQueryTile) continue;
-      const int s = is[k];
+      const int s = is(k);
       const int l = l0 + qi;
       const int64_t qh = ((int64_t)bb * a.L + l) * a.H + h;
       a.weights[bb * a.wsb + (int64_t)l * a.wsl + h * a.wsh + s] = wgt[k];
@@ -725,7 +766,7 @@ __global__ __launch_bounds__(256, 2) void sample_kernel(SampleArgs a) {
       const int ncols = min(kLevelCols, ps.level_cols(d) - c0);
 #pragma unroll
       for (int k = 0; k < kNI; ++k) {
-        const int qi = wk.iq[k];
+        const int qi = wk.iq(k);
         if (qi >= kQueryTile) continue;
         const int base = (wk.node[k] << lb) - c0;
         if (base < 0 || base >= ncols) continue;
@@ -789,15 +830,22 @@ __global__ __launch_bounds__(256) void sample_sparse_kernel(SampleArgs a) {
     constexpr int DPL = D / 16;  // head dims per lane: 2, 4, 6 or 8
     const int j16 = lane & 15, r0 = lane & 48;
     const int nrow = a.pair_rows ? 1 : kB;
+    // each wave's items (query, node) in LDS past the query rows, so a row's
+    // 16 lanes read item m with one broadcast load; a wave reads only its own
+    // entries, which LDS orders after its writes
+    static_assert(kQueryTile * (D + 4) * 4 + 4 * kNI * 64 * 8 <= kQueryTile * kXS * 4, "item table fits");
+    int2* tab = (int2*)(qs + kQueryTile * QS) + (tid >> 6) * kNI * 64;
     for (int dd = Td; dd < T; ++dd) {
       const float* lvl = a.sum32 + ((int64_t)bh * G.NS + G.off[dd + 1]) * D + DPL * j16;
+#pragma unroll
+      for (int k = 0; k < kNI; ++k) tab[k * 64 + lane] = make_int2(wk.iq(k), wk.node[k]);
 #pragma unroll
       for (int k = 0; k < kNI; ++k) {
         float part[kB][16];
 #pragma unroll
         for (int m = 0; m < 16; ++m) {
-          const int qm = __shfl(wk.iq[k], r0 + m, 64);
-          const int nm = __shfl(wk.node[k], r0 + m, 64);
+          const int2 it = tab[k * 64 + r0 + m];
+          const int qm = it.x, nm = it.y;
           const bool act = qm < kQueryTile;
           const float* qrow = qs + (act ? qm : 0) * QS + DPL * j16;
           float qv[DPL];
@@ -825,7 +873,7 @@ __global__ __launch_bounds__(256) void sample_sparse_kernel(SampleArgs a) {
 #pragma unroll
         for (int j = 0; j < kB; ++j) xo[j] = row_reduce_scatter16(part[j], j16);
         if (a.pair_rows) xo[1] = -xo[0];
-        if (wk.iq[k] < kQueryTile) wk.decide(a, logA, k, dd, xo);
+        if (wk.iq(k) < kQueryTile) wk.decide(a, logA, k, dd, xo);
       }
     }
     __syncthreads();  // qs (Xs) is reused below
@@ -895,14 +943,18 @@ template <bool kReplay, typename E, int D>
 static hipError_t sample_b(const Plan& P, const void* q, const float* U, uint64_t seed, float* w, char* rec,
                            hipStream_t st, const uint8_t* pa) {
   static_assert(kMaxSamples * kQueryTile / 256 == 16, "items per thread");
-  const bool few = P.S <= 16;  // 64 * S / 256 <= 4 items per thread
+  // 64 * S / 256 items per thread: 4 (S <= 16), 8 (S <= 32) or 16
+  const int ni = P.S <= 16 ? 4 : P.S <= 32 ? 8 : 16;
   switch (P.geo.b) {
-    case 2: return few ? sample_impl<kReplay, E, D, 2, 4>(P, q, U, seed, w, rec, st, pa)
-                       : sample_impl<kReplay, E, D, 2, 16>(P, q, U, seed, w, rec, st, pa);
-    case 4: return few ? sample_impl<kReplay, E, D, 4, 4>(P, q, U, seed, w, rec, st, pa)
-                       : sample_impl<kReplay, E, D, 4, 16>(P, q, U, seed, w, rec, st, pa);
-    default: return few ? sample_impl<kReplay, E, D, 0, 4>(P, q, U, seed, w, rec, st, pa)
-                        : sample_impl<kReplay, E, D, 0, 16>(P, q, U, seed, w, rec, st, pa);
+    case 2: return ni == 4 ? sample_impl<kReplay, E, D, 2, 4>(P, q, U, seed, w, rec, st, pa)
+                 : ni == 8 ? sample_impl<kReplay, E, D, 2, 8>(P, q, U, seed, w, rec, st, pa)
+                           : sample_impl<kReplay, E, D, 2, 16>(P, q, U, seed, w, rec, st, pa);
+    case 4: return ni == 4 ? sample_impl<kReplay, E, D, 4, 4>(P, q, U, seed, w, rec, st, pa)
+                 : ni == 8 ? sample_impl<kReplay, E, D, 4, 8>(P, q, U, seed, w, rec, st, pa)
+                           : sample_impl<kReplay, E, D, 4, 16>(P, q, U, seed, w, rec, st, pa);
+    default: return ni == 4 ? sample_impl<kReplay, E, D, 0, 4>(P, q, U, seed, w, rec, st, pa)
+                  : ni == 8 ? sample_impl<kReplay, E, D, 0, 8>(P, q, U, seed, w, rec, st, pa)
+                            : sample_impl<kReplay, E, D, 0, 16>(P, q, U, seed, w, rec, st, pa);
   }
 }
 

@@ -1419,7 +1419,12 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     return hipSuccess;
   };
   hipError_t e = hipSuccess;
-  if (P.S > 16) e = launch_dq(tree_dq_kernel<E, D, 64, 0>);
+  if (P.S > 32 && P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 64, 2>);
+  else if (P.S > 32 && P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 64, 4>);
+  else if (P.S > 32) e = launch_dq(tree_dq_kernel<E, D, 64, 0>);
+  else if (P.S > 16 && P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 32, 2>);
+  else if (P.S > 16 && P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 32, 4>);
+  else if (P.S > 16) e = launch_dq(tree_dq_kernel<E, D, 32, 0>);
   else if (P.S <= 8 && P.geo.b == 2) e = launch_dq(tree_dq_kernel<E, D, 8, 2>);  // half the scan lanes
   else if (P.S <= 8 && P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 8, 4>);
   else if (P.geo.b == 4) e = launch_dq(tree_dq_kernel<E, D, 16, 4>);
