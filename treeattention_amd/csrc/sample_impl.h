@@ -615,7 +615,11 @@ struct Walk {
 // kNI: (query, sample) items per thread, >= 64 * S / 256.
 // kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
 template <typename E, int D, int kB, int kNI, bool kReplay>
-__global__ __launch_bounds__(256, 2) void sample_kernel(SampleArgs a) {
+// Binary trees with 16 items per thread at head dims of 96 and up spill at
+// two waves per SIMD; one wave with the whole register file runs them faster
+// (the reference tree at L = 16384, 64 paths: 5.85 -> 4.14 ms; branching 4
+// is faster at two waves).
+__global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) void sample_kernel(SampleArgs a) {
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
