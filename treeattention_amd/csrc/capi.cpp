@@ -128,7 +128,12 @@ int make_plan(const ta_problem* p, Plan* P) {
   // Likewise the backward's dense G tiles (and their G^T rows in the
   // workspace) cover levels with at most kTreeDenseCols children; deeper ones
   // run in the band kernels, linear in the sampled pairs.
-  const int64_t tcols = p->dense_cols > 0 ? p->dense_cols : kTreeDenseCols;
+  // Deep binary trees (the reference tree at L >= 16384) run their widest dense
+  // levels in bands too: the tree backward at L = 16384 takes 5.23 ms with
+  // levels up to 512 children dense against 6.05 ms up to 1024, and at
+  // L = 65536 31.9 ms up to 256 against 38.8 ms up to 1024.
+  const int64_t tdef = (b == 2 && T >= 16) ? 256 : (b == 2 && T >= 14) ? 512 : kTreeDenseCols;
+  const int64_t tcols = p->dense_cols > 0 ? p->dense_cols : tdef;
   P->tree_dense = T;
   if (b == 2 || b == 4)
     for (int d = 0; d < T; ++d)
