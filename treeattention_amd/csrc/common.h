@@ -394,6 +394,30 @@ inline unsigned group_grid(int64_t nbh, int nl) {
   return nbh >= kXcds ? xcd_grid(nbh, nl) : (unsigned)(nbh * nl);
 }
 
+// ------------------------------------------------------- DPP exchanges ---
+// x from lane (i - R) mod 16 of the same 16-lane row (DPP row_ror).
+template <int R>
+__device__ __forceinline__ float dpp_row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + R, 0xf, 0xf, false));
+}
+// x from lane j ^ M of this 16-lane row (M = 1, 2, 4, 8; j = lane & 15), by
+// DPP moves: quad_perm [1, 0, 3, 2] for M = 1, [2, 3, 0, 1] for M = 2, a
+// rotation by 8 for M = 8, and for M = 4 the rotation by 4 or by 12, whichever
+// lands on j ^ 4.  No LDS traffic, unlike a shuffle.
+template <int M>
+__device__ __forceinline__ float row_xor(float x, int j) {
+  if constexpr (M == 1) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+  } else if constexpr (M == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));
+  } else if constexpr (M == 8) {
+    return dpp_row_ror<8>(x);
+  } else {
+    const float dn = dpp_row_ror<M>(x), up = dpp_row_ror<16 - M>(x);
+    return (j & M) ? dn : up;
+  }
+}
+
 // ------------------------------------------------------ vector-ALU dots ---
 
 __device__ __forceinline__ float logsig(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }

@@ -206,20 +206,6 @@ __device__ __forceinline__ void row_dups16(int n, float e, int s, float& tot, bo
     row_dups16<R + 1>(n, e, s, tot, fst);
   }
 }
-// x from lane j ^ M of this 16-lane row (M = 1, 2, 4, 8), by DPP moves:
-// quad_perm [1, 0, 3, 2] for M = 1, a rotation by 8 for M = 8, else the
-// rotation by M or by 16 - M, whichever lands on j ^ M.
-template <int M>
-__device__ __forceinline__ float row_xor(float x, int j) {
-  if constexpr (M == 1) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
-  } else if constexpr (M == 8) {
-    return row_ror<8>(x);
-  } else {
-    const float dn = row_ror<M>(x), up = row_ror<16 - M>(x);
-    return (j & M) ? dn : up;
-  }
-}
 // Lane j of each 16-lane row holds p[m] = its part of item m's sum (m < 16);
 // returns item j's total (sum over the row's lanes of p[j]), by halving
 // exchanges with lanes j ^ 8, j ^ 4, j ^ 2, j ^ 1.

@@ -1156,9 +1156,9 @@ __global__ __launch_bounds__(256, 2) void tree_band_kernel(BandArgs a) {
           const float4 cv = *(const float4*)(cr + (int64_t)c * D + i);
           p += qv[i] * cv.x + qv[i + 1] * cv.y + qv[i + 2] * cv.z + qv[i + 3] * cv.w;
         }
-        p += __shfl_xor(p, 1, 64);
-        p += __shfl_xor(p, 2, 64);
-        p += __shfl_xor(p, 4, 64);
+        p += row_xor<1>(p, lane & 15);  // the pair's eight lanes
+        p += row_xor<2>(p, lane & 15);
+        p += row_xor<4>(p, lane & 15);
         x[c] = p;
       }
       if (!rep) continue;
