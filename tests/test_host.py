@@ -56,6 +56,24 @@ def test_struct_layout_and_sizes():
     assert ns == 32 + 32 + 64 + 256  # levels 4, 16, 64, 256 padded to 32 rows
 
 
+def test_path_rows_layout():
+    """16-bit problems with b = 2 or 4 and T*b <= 32 take the tree gradient along each pair's
+    path in the leaf backward: the record keeps the float output (dout . out in the backward)
+    and the backward workspace drops the dense G^T tiles; dense_cols > 0 keeps the dense
+    levels, float inputs and one-token leaves always do."""
+    out32 = 2 * 16384 * 16 * 128 * 4
+    sum_t = 32 * (32 + 32 + 64 + 256) * 128 * 2  # the dense backward's transposed summaries
+    rec_p, fws_p, bws_p = _lib.byte_sizes(_problem())
+    rec_d, fws_d, bws_d = _lib.byte_sizes(_problem(dense_cols=1024))
+    assert rec_p == rec_d + out32 - sum_t and fws_p == fws_d
+    assert bws_p < bws_d
+    # C4's shape (128-key blocks, head dim 128) keeps the dense levels
+    c4 = dict(B=1, L=131072, N=131072, H=8, leaf_block=128, branching=2, causal=0)
+    assert _lib.byte_sizes(_problem(**c4)) == _lib.byte_sizes(_problem(dense_cols=1024, **c4))
+    f32 = dict(dtype=_lib.TA_F32, D=64)
+    assert _lib.byte_sizes(_problem(**f32)) == _lib.byte_sizes(_problem(dense_cols=1024, **f32))
+
+
 @pytest.mark.parametrize("D,LB", [(128, 64), (96, 64), (96, 128), (64, 128), (32, 128), (128, 128)])
 def test_float_leaf_tiles_fit(D, LB):
     """fp32 inputs with large head dims or blocks run the leaf backward with 32- or 16-pair
@@ -85,7 +103,8 @@ def test_many_samples_run_in_chunks():
     sample's leaf block and the float output; workspaces are reused chunk after chunk."""
     one = _lib.byte_sizes(_problem(num_samples=64))
     two = _lib.byte_sizes(_problem(num_samples=128))
-    assert two[0] > 2 * one[0]          # two chunk records + leaves + float output
+    out32 = 2 * 16384 * 16 * 128 * 4    # the float output, kept once per problem
+    assert two[0] > 2 * one[0] - out32  # two chunk records + leaves + float output
     assert two[1] == one[1]             # chunks of 64: the same forward workspace
     assert two[2] > one[2]              # + float accumulators
     lo = _lib.record_offset(_problem(num_samples=128), _lib.TA_REC_LEAVES)

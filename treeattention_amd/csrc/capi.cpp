@@ -47,7 +47,7 @@ bool strides_ok(const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2
 }  // namespace
 
 // Builds and validates the plan; returns TA_OK or an error code (message set).
-int make_plan(const ta_problem* p, Plan* P) {
+int make_plan(const ta_problem* p, Plan* P, bool chunk) {
   if (!p) return fail(TA_ERR_INVALID, "problem is NULL");
   P->p = *p;
   const int64_t B = p->B, L = p->L, N = p->N, H = p->H, D = p->D, S = p->num_samples;
@@ -177,11 +177,25 @@ int make_plan(const ta_problem* p, Plan* P) {
   const int64_t BLHS = B * L * H * S;
   const int64_t es = P->esize;
   const bool half = es == 2;
+  // The tree gradient along each pair's path inside the leaf backward (its T*b
+  // child rows are one more MFMA tile per pair tile): 16-bit inputs, leaf
+  // blocks of two or more tokens, b = 2 or 4 with T*b <= 32, not the
+  // reference causal mode, dense_cols at its default, and the leaf tile with
+  // the path rows inside the LDS.  Otherwise the dense level tiles and bands.
+  // (128-key blocks with head dims of 96 or more already fill the 256 registers
+  // of the leaf tile's waves: those keep the dense levels)
+  P->path_rows = 0;
+  if (half && LB > 1 && (b == 2 || b == 4) && T >= 1 && T * b <= 32 && p->causal != TA_CAUSAL_REFERENCE &&
+      p->dense_cols == 0 && !(LB > 64 && D >= 96)) {
+    P->path_rows = T * b <= 16 ? 16 : 32;
+    if (leaf_bwd_smem(*P) < 0) P->path_rows = 0;
+  }
+  const bool pr = P->path_rows > 0;
   Carver r;
   P->rec.summaries = r.take(P->BH * G.NS * D * 4);
   P->rec.sum_hi = r.take(half ? P->BH * G.NS * D * es : 0);
   P->rec.sum_lo = r.take(half ? P->BH * G.NS * D * es : 0);
-  P->rec.sum_t = r.take(P->BH * G.NS * D * es);
+  P->rec.sum_t = r.take(pr ? 0 : P->BH * G.NS * D * es);  // the dense backward's transposed copy
   P->rec.means = r.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : P->BH * NL * D * 4);
   P->rec.segs = r.take(p->tree_mode == TA_TREE_NODEKEYS || NL < 128 ? 0 : P->BH * (NL / 64 + NL / 4096) * D * 4);
   P->rec.leaf = r.take(BLHS * 4);
@@ -202,20 +216,23 @@ int make_plan(const ta_problem* p, Plan* P) {
   P->rec.sort_keys = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
   P->rec.sort_vals = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
   P->rec.sort_hist = r.take(P->bucket_sort ? 256 * ((BLHS + 2047) / 2048 + 1) * 4 : 0);
+  P->rec.out32 = r.take(pr && !chunk ? B * L * H * D * 4 : 0);
   P->rec.total = r.at;
   const bool lb1 = LB == 1;  // leaf stage: a value gather, no pair rows
   Carver f;
   P->fws.partial = f.take(lb1 ? 0 : BLHS * D * es);
   P->fws.total = f.at;
   Carver w;
-  P->bws.delta = w.take(BLHS * 4);
+  P->bws.delta = w.take(pr ? 0 : BLHS * 4);
   P->bws.dq_part = w.take(!lb1 || P->tree_dense < T ? BLHS * D * es : 0);
-  P->bws.dlogp = w.take(BLHS * 4);
+  P->bws.dlogp = w.take(pr ? 0 : BLHS * 4);
   P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS || lb1 ? 0 : B * N * H * D * 4);
-  P->bws.gt = w.take(P->BH * NSd * P->Lp * es);
-  P->bws.qt = w.take(P->BH * D * P->Lp * es);
-  P->bws.dsum_part = w.take(qsplit * P->BH * NSd * D * 4);
+  P->bws.gt = w.take(pr ? 0 : P->BH * NSd * P->Lp * es);
+  P->bws.qt = w.take(pr ? 0 : P->BH * D * P->Lp * es);
+  P->bws.dsum_part = w.take(pr ? 0 : qsplit * P->BH * NSd * D * 4);
   P->bws.dsum = w.take(P->BH * G.NS * D * 4);
+  P->bws.mean = w.take(pr ? B * L * H * 4 : 0);
+  P->bws.dcp = w.take(pr ? P->BH * NL * T * b * D * 4 : 0);
   const bool rc = p->causal == TA_CAUSAL_REFERENCE;
   P->bws.rc_coef = w.take(rc ? B * L * H * T * 4 : 0);
   P->bws.rc_rho = w.take(rc ? B * L * H * T * 4 : 0);
@@ -262,7 +279,7 @@ int make_chunks(const ta_problem* p, Chunks* C) {
   for (int g = 0; g < n; ++g) {
     ta_problem pg = *p;
     pg.num_samples = S / n + (g < S % n ? 1 : 0);
-    const int rc = make_plan(&pg, &C->P[g]);
+    const int rc = make_plan(&pg, &C->P[g], true);
     if (rc) return rc;
     Plan& P = C->P[g];
     P.s0 = s0;

@@ -52,37 +52,52 @@ hipError_t launch_chunk_merge(const Plan& P, const ChunkRecs& R, float* weights,
   return hipGetLastError();
 }
 
-// mean[b, l, h] = dout[b, l, h, :] . out32[b, l, h, :]; one thread per row.
-template <typename E>
+// mean[b, l, h] = dout[b, l, h, :] . out32[b, l, h, :]; a group of DG lanes
+// per row (DG = D / 8 rounded up to a power of two), eight dims per lane in
+// 16-byte loads, then a butterfly over the group (a fixed order).
+template <typename E, int DG>
 __global__ __launch_bounds__(256) void chunk_mean_kernel(const E* __restrict__ g, int64_t gsb, int64_t gsl,
                                                          int64_t gsh, const float* __restrict__ out32,
                                                          float* __restrict__ mean, int L, int H, int D, int64_t nqh) {
-  const int64_t qh = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (qh >= nqh) return;
-  const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
-  const E* gr = g + bb * gsb + l * gsl + h * gsh;
-  const float* o = out32 + qh * D;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t qh = gid / DG;
+  const int dg = (int)(gid - qh * DG);
   float s = 0.f;
-  for (int d = 0; d < D; ++d) s += (float)gr[d] * o[d];
-  mean[qh] = s;
+  if (qh < nqh && 8 * dg < D) {
+    const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
+    float gv[8];
+    ld8f(gv, g + bb * gsb + l * gsl + h * gsh + 8 * dg);
+    const float* o = out32 + qh * D + 8 * dg;
+    const float4 o0 = *(const float4*)o, o1 = *(const float4*)(o + 4);
+    s = gv[0] * o0.x + gv[1] * o0.y + gv[2] * o0.z + gv[3] * o0.w + gv[4] * o1.x + gv[5] * o1.y + gv[6] * o1.z +
+        gv[7] * o1.w;
+  }
+#pragma unroll
+  for (int m = 1; m < DG; m <<= 1) s += __shfl_xor(s, m, 64);
+  if (qh < nqh && dg == 0) mean[qh] = s;
+}
+
+template <typename E, int DG>
+static void mean_launch(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
+  const int64_t nqh = P.B * P.L * P.H;
+  const dim3 grid((unsigned)((nqh * DG + 255) / 256));
+  const int64_t* gs = P.p.g_strides;
+  hipLaunchKernelGGL((chunk_mean_kernel<E, DG>), grid, dim3(256), 0, st, (const E*)g, gs[0], gs[1], gs[2], out32,
+                     mean, (int)P.L, (int)P.H, (int)P.D, nqh);
+}
+
+template <typename E>
+static void mean_d(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
+  if (P.D <= 32) mean_launch<E, 4>(P, g, out32, mean, st);
+  else if (P.D <= 64) mean_launch<E, 8>(P, g, out32, mean, st);
+  else mean_launch<E, 16>(P, g, out32, mean, st);
 }
 
 hipError_t launch_chunk_mean(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
-  const int64_t nqh = P.B * P.L * P.H;
-  const dim3 grid((unsigned)((nqh + 255) / 256));
-  const int64_t* gs = P.p.g_strides;
   switch (P.p.dtype) {
-    case TA_F32:
-      hipLaunchKernelGGL(chunk_mean_kernel<float>, grid, dim3(256), 0, st, (const float*)g, gs[0], gs[1], gs[2],
-                         out32, mean, (int)P.L, (int)P.H, (int)P.D, nqh);
-      break;
-    case TA_BF16:
-      hipLaunchKernelGGL(chunk_mean_kernel<bf16>, grid, dim3(256), 0, st, (const bf16*)g, gs[0], gs[1], gs[2],
-                         out32, mean, (int)P.L, (int)P.H, (int)P.D, nqh);
-      break;
-    default:
-      hipLaunchKernelGGL(chunk_mean_kernel<f16>, grid, dim3(256), 0, st, (const f16*)g, gs[0], gs[1], gs[2], out32,
-                         mean, (int)P.L, (int)P.H, (int)P.D, nqh);
+    case TA_F32: mean_d<float>(P, g, out32, mean, st); break;
+    case TA_BF16: mean_d<bf16>(P, g, out32, mean, st); break;
+    default: mean_d<f16>(P, g, out32, mean, st);
   }
   return hipGetLastError();
 }

@@ -176,6 +176,20 @@ __device__ __forceinline__ typename Mfma<E>::frag acc_operand(const f32x4 (&acc)
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Eight consecutive elements (16-byte aligned) as floats.
+template <typename E>
+__device__ __forceinline__ void ld8f(float* o, const E* p) {
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(8))) E e8;
+    const e8 v = *(const e8*)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (float)v[i];
+  } else {
+    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
+    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+  }
+}
+
 // dst[0..8) = v (first) or dst + v: float rows summed over the sample chunks
 // of a problem with many samples (16-byte aligned dst).
 __device__ __forceinline__ void acc8f(float* dst, const float* v, int first) {
@@ -564,6 +578,7 @@ struct RecordLayout {
   int64_t sort_keys;   // uint32 (2, B, L, H, S): bucketing by sort, key double buffer
   int64_t sort_vals;   // int (2, B, L, H, S): bucketing by sort, value double buffer
   int64_t sort_hist;   // int (256, tiles of 2048 keys + 1): the sort's per-tile digit counts, digit totals
+  int64_t out32;       // float (B, L, H, D): the forward output before rounding (path rows, one chunk)
   int64_t total;
 };
 
@@ -584,6 +599,8 @@ struct BwdWorkspaceLayout {
   int64_t rc_coef;   // float (B, L, H, T): reference causal mode, boundary-mass gradient scale
   int64_t rc_rho;    // float (B, L, H, T): reference causal mode, on-path share of each boundary mass
   int64_t rc_g;      // float (B, L, H, T): reference causal mode, boundary children's gradient (band depths)
+  int64_t mean;      // float (B, L, H): path rows, dout . out over the query's samples
+  int64_t dcp;       // float (BH, NL, T*b, D): path rows, each leaf block's gradient of its path's children
   int64_t total;
 };
 

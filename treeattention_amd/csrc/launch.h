@@ -35,6 +35,8 @@ struct Plan {
   int sample_dense; // the sampler's level tiles cover depths < sample_dense; deeper levels are sparse
   int tree_dense;   // the backward's dense G tiles cover depths < tree_dense; deeper ones run in bands
   int bucket_sort;  // many leaf blocks: bucketing by a radix sort of (batch * head, leaf block) keys
+  int path_rows;    // > 0: the leaf backward adds the tree gradient along each pair's path (T*b rows,
+                   // padded to 16 or 32); the tree backward only sums rows and blocks
   int64_t s0, s_total;  // this plan's samples are s0 .. s0 + S - 1 of s_total (uniform / path indices)
   ChunkAcc acc;
   RecordLayout rec;
@@ -60,7 +62,9 @@ struct Chunks {
 };
 
 // capi.cpp: plan builder and the calling thread's error message
-int make_plan(const ta_problem* p, Plan* P);  // TA_OK or an error code (message set)
+// TA_OK or an error code (message set); chunk: a chunk of a problem with many
+// samples (whose float output lives in the problem's record, not the chunk's)
+int make_plan(const ta_problem* p, Plan* P, bool chunk = false);
 int make_chunks(const ta_problem* p, Chunks* C);
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();  // clears the message, returns TA_OK

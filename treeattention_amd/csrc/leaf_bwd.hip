@@ -12,28 +12,10 @@
 //   dz = w P (dP - delta)
 //   dq_pair^T = scale K^T dz^T                     (-> per-pair slot, summed in tree_bwd)
 //   dV += (w P)^T g,  dK += scale dz^T Q            (P^T and dz^T staged in LDS)
-#include "launch.h"
+#include "leaf_bwd_tr.h"
 
 namespace ta {
 
-struct LeafBwdArgs {
-  int B, L, N, H, S, NL, LB, causal;
-  float scale, scale_log2;
-  const void *q, *k, *v, *g;
-  int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh, gsb, gsl, gsh;
-  const int* order;
-  const int* block_start;
-  const float* slot_weight;
-  float* delta;     // (B,L,H,S)
-  void* dq_part;    // E (B,L,H,S,D)
-  void* dv;         // E, v strides
-  float* dk_leaf;   // (B,N,H,D) or null
-  float* dv32;      // chunked problem: dv as float (B,N,H,D) rows, else null
-  int first;        // chunked problem: the first chunk writes dv32 / dk_leaf, later ones add
-};
-
-// One element of the float accumulators of a chunked problem (or of dk_leaf).
-__device__ __forceinline__ void acc1f(float* p, float x, int first) { *p = first ? x : *p + x; }
 
 template <typename E>
 __device__ __forceinline__ void mov8(E* o, const E* p) {
@@ -280,303 +262,6 @@ __global__ __launch_bounds__(256) void leaf_bwd_kernel(LeafBwdArgs a) {
   }
 }
 
-// Transposing-read variant for 16-bit inputs: eight waves and 128-pair tiles
-// (four waves and 64-pair tiles for 128-key blocks).  Phase A (each wave,
-// its 16 pairs): query and output-gradient rows come straight from global
-// memory into MFMA fragments (the next tile's are loaded while this one
-// computes), then P, delta, dz and the pair's dq; the wave then stores its
-// rows of Q, dout, wP and dz into row-major LDS tiles with 16- and 8-byte
-// writes.  Phase B (all waves, each a block of output tiles): dV += (wP)^T dout
-// and dK += dz^T Q over the tile's pairs.  The MFMA operands of phase B and
-// K^T of the dq product are read with ds_read_b64_tr_b16, gfx950's transposing
-// LDS read: within each group of 16 lanes, lane i receives element i%4 of the
-// 8-byte slots of lanes 4r + i/4 (r = 0..3), so pointing lane j of a group at
-// row k0 + j/4, columns 4(j%4).. of a row-major [k][n] tile gives lane i the
-// four values [k0..k0+3][n = i] -- a k-contiguous operand column.  Row strides
-// are padded by 16 elements so every 16-lane group touches distinct banks.
-// Eight waves.  Leaf blocks of up to 64 keys take 128-pair tiles, 16 pairs
-// per wave; 128-key blocks take 64-pair tiles (so the K / V, pair-row and
-// P / dz tiles fit the LDS), whose phase A runs on waves 0-3 while all eight
-// share phase B.
-template <int D, int LBP>
-struct BwdTrTile {
-  static constexpr int NW = 8;                      // waves
-  static constexpr int QT = LBP > 64 ? 64 : 128;    // pairs per tile, 16 per phase-A wave
-  static constexpr int RS = D + 16, PS = LBP + 16;
-  static constexpr int bytes = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
-};
-
-
-// One pair column's operands for a tile: query and output-gradient row
-// fragments, the pair's summed sample weight, its query row (-1: padding) and
-// its (b, l, h, u) slot.
-template <typename E, int D>
-struct PairRows {
-  RowFrags<E, D> q, g;
-  float w;
-  int l;
-  int64_t sl;
-  // Waits here for the loads of this set; no memory operation moves above.
-  __device__ __forceinline__ void pin() const {
-    q.pin();
-    g.pin();
-    pin_value(w);
-  }
-};
-
-template <typename E, int D, int LBP>
-__global__ __launch_bounds__((64 * BwdTrTile<D, LBP>::NW)) void leaf_bwd_tr_kernel(LeafBwdArgs a) {
-  static_assert(sizeof(E) == 2, "16-bit inputs");
-  using M = Mfma<E>;
-  using BT = BwdTrTile<D, LBP>;
-  constexpr int QT = BT::QT, RS = BT::RS, PS = BT::PS;
-  constexpr int NW = BT::NW;
-  extern __shared__ __align__(16) char smem[];
-  E* Ks = (E*)smem;        // [LBP][RS]
-  E* Vs = Ks + LBP * RS;   // [LBP][RS]
-  E* Qs = Vs + LBP * RS;   // [QT][RS]  Q rows of the tile
-  E* Gs = Qs + QT * RS;    // [QT][RS]  dout rows of the tile
-  E* Ps = Gs + QT * RS;    // [QT][PS]  w P rows
-  E* Zs = Ps + QT * PS;    // [QT][PS]  dz rows
-
-  int bh, beta;
-  if (!xcd_bh_block(blockIdx.x, a.B * a.H, a.NL, bh, beta)) return;
-  const int bb = bh / a.H, h = bh - bb * a.H;
-  const int* bs = a.block_start + (int64_t)bh * (a.NL + 1);
-  const int start = bs[beta], end = bs[beta + 1];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, g = lane >> 4;
-  const int LB = a.LB, S = a.S;
-  const int64_t LS = (int64_t)a.L * S;
-  const E* q = (const E*)a.q;
-  const E* k = (const E*)a.k;
-  const E* v = (const E*)a.v;
-  const E* go = (const E*)a.g;
-
-  {  // stage the block's K and V rows: every load issued before the first LDS write
-    constexpr int NST = (LBP * D / 8 + NW * 64 - 1) / (NW * 64);
-    uint4 kr[NST], vr[NST];
-#pragma unroll
-    for (int i = 0; i < NST; ++i) {
-      const int e = tid + i * NW * 64;
-      const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
-      const int64_t tok = (int64_t)beta * LB + key;
-      const bool in = e < LBP * D / 8 && key < LB;
-      kr[i] = in && k ? *(const uint4*)(k + bb * a.ksb + tok * a.ksl + h * a.ksh + c) : make_uint4(0, 0, 0, 0);
-      vr[i] = in ? *(const uint4*)(v + bb * a.vsb + tok * a.vsl + h * a.vsh + c) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < NST; ++i) {
-      const int e = tid + i * NW * 64;
-      const int key = e / (D / 8), c = (e - key * (D / 8)) * 8;
-      if (e < LBP * D / 8) {
-        *(uint4*)(Ks + key * RS + c) = kr[i];
-        *(uint4*)(Vs + key * RS + c) = vr[i];
-      }
-    }
-  }
-  __syncthreads();
-
-  // phase B: waves 0-3 accumulate dV = (wP)^T dout, waves 4-7 dK = dz^T Q;
-  // wave w & 3 owns the quarter (key half (w & 3) >> 1, dim half w & 1):
-  // MK2 x ND2 tiles of 16 x 16, MK2 + ND2 operand reads per MK2 * ND2 MFMAs
-  constexpr int MK2 = LBP / 32, ND2 = D / 32;
-  const bool dkw = w >= 4;
-  const int mkb = MK2 * ((w & 3) >> 1), ndb = ND2 * (w & 1);
-  const E* Ab = dkw ? Zs : Ps;
-  const E* Bb = dkw ? Qs : Gs;
-  f32x4 acc[MK2][ND2];
-#pragma unroll
-  for (int x = 0; x < MK2; ++x)
-#pragma unroll
-    for (int y = 0; y < ND2; ++y) acc[x][y] = zero4();
-
-  // Software pipeline over QT-pair tiles with two register sets: a tile
-  // first waits for its own set (loaded one tile earlier), then issues the
-  // loads of the next tile into the other set and reads the pair index of the
-  // tile after.  The wait sits before the new loads on purpose: vmcnt counts
-  // loads and stores alike, so any wait placed after them would also wait for
-  // them.  The loop is unrolled twice so the sets never move between registers.
-  const int* ord = a.order + (int64_t)bh * LS;
-  const int pcol = 16 * w + col;  // this lane's pair column within the tile
-  const bool aw = QT == 16 * NW || 16 * w < QT;  // the wave has pairs (phase A)
-  auto idx = [&](int t) { return aw && t + pcol < end ? ord[t + pcol] : -1; };
-  auto fetch = [&](int e, PairRows<E, D>& r) {  // pair entry e = l * S + u, or -1
-    const int l = e >= 0 ? e / S : 0;
-    r.l = e >= 0 ? l : -1;
-    r.sl = (((int64_t)bb * a.L + l) * a.H + h) * S + (e >= 0 ? e - l * S : 0);
-    r.q.load(e >= 0 ? q + bb * a.qsb + (int64_t)l * a.qsl + h * a.qsh : nullptr, g);
-    r.g.load(e >= 0 ? go + bb * a.gsb + (int64_t)l * a.gsl + h * a.gsh : nullptr, g);
-    r.w = e >= 0 ? a.slot_weight[r.sl] : 0.f;
-  };
-  auto tile = [&](const PairRows<E, D>& c) {
-    const bool valid = c.l >= 0;
-    const int l = valid ? c.l : 0;
-    const int64_t sl = c.sl;
-    const float wt = c.w;
-    const RowFrags<E, D>& qc = c.q;
-    const RowFrags<E, D>& gc = c.g;
-
-    // ---- phase A: this wave's 16 pairs
-    f32x4 sacc[LBP / 16], pacc[LBP / 16];
-    if (aw) {
-#pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt) {
-      sacc[mt] = zero4();
-      pacc[mt] = zero4();
-      const E* kp = Ks + (16 * mt + col) * RS + M::KPL * g;
-      const E* vp = Vs + (16 * mt + col) * RS + M::KPL * g;
-#pragma unroll
-      for (int ks = 0; ks < D / M::K; ++ks) {
-        sacc[mt] = M::mma(ld_frag(kp + ks * M::K), qc.f[ks], sacc[mt]);
-        pacc[mt] = M::mma(ld_frag(vp + ks * M::K), gc.f[ks], pacc[mt]);
-      }
-    }
-    // keys < kmax are visible; masking only when some pair of the tile needs it
-    const int kmax = valid ? (a.causal ? min(LB, l + (a.N - a.L) - beta * LB + 1) : LB) : 0;
-    if (__any(kmax < LBP)) {
-#pragma unroll
-      for (int mt = 0; mt < LBP / 16; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sacc[mt][r] = (16 * mt + 4 * g + r) < kmax ? sacc[mt][r] * a.scale_log2 : -__builtin_inff();
-    } else {
-#pragma unroll
-      for (int mt = 0; mt < LBP / 16; ++mt) sacc[mt] *= a.scale_log2;
-    }
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt)
-      mx = fmaxf(mx, fmaxf(fmaxf(sacc[mt][0], sacc[mt][1]), fmaxf(sacc[mt][2], sacc[mt][3])));
-    mx = col_max(mx);
-    if (mx == -__builtin_inff()) mx = 0.f;  // no visible key (padding pairs): all p = 0
-    float sum = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(sacc[mt][r] - mx);
-        sacc[mt][r] = pv;
-        sum += pv;
-      }
-    sum = col_sum(sum);
-    const float inv = sum > 0.f ? __builtin_amdgcn_rcpf(sum) : 0.f;
-    float delta = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sacc[mt][r] *= inv;
-        delta += sacc[mt][r] * pacc[mt][r];
-      }
-    delta = col_sum(delta);
-#pragma unroll
-    for (int mt = 0; mt < LBP / 16; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pacc[mt][r] = wt * sacc[mt][r] * (pacc[mt][r] - delta);
-    if (valid && g == 0) a.delta[sl] = delta;
-
-    // dq_pair^T = K^T dz^T: K^T fragments read transposed from Ks in the
-    // accumulator's key order (keys 32ks + 4g.. and 32ks + 16 + 4g..)
-    // K^T fragments with permuted head dims: each lane ends with eight
-    // consecutive dims of its pair's dq row, one 16-byte store per 32 dims
-    E* dqp = (E*)a.dq_part + sl * D + 8 * g;
-#pragma unroll
-    for (int p = 0; p < D / 32; ++p) {
-      f32x4 o0 = zero4(), o1 = zero4();
-#pragma unroll
-      for (int ks = 0; ks < LBP / M::K; ++ks) {
-        const typename M::frag z = acc_operand<E>(pacc, ks);
-        o0 = M::mma(perm_dim_frag<E>(Ks, RS, 2 * p, ks, lane), z, o0);
-        o1 = M::mma(perm_dim_frag<E>(Ks, RS, 2 * p + 1, ks, lane), z, o1);
-      }
-      if (valid) {
-        typedef __attribute__((ext_vector_type(8))) E e8;
-        e8 o;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          o[r] = (E)(o0[r] * a.scale);
-          o[4 + r] = (E)(o1[r] * a.scale);
-        }
-        *(e8*)(dqp + 32 * p) = o;
-      }
-    }
-
-    }  // aw
-
-    __syncthreads();  // phase B of the previous tile is done with the staging tiles
-    if (aw) {
-      E* pr = Ps + pcol * PS + 4 * g;
-      E* zr = Zs + pcol * PS + 4 * g;
-#pragma unroll
-      for (int mt = 0; mt < LBP / 16; ++mt) {
-        typedef __attribute__((ext_vector_type(4))) E e4;
-        e4 pv, zv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pv[r] = (E)(wt * sacc[mt][r]);
-          zv[r] = (E)pacc[mt][r];
-        }
-        *(e4*)(pr + 16 * mt) = pv;
-        *(e4*)(zr + 16 * mt) = zv;
-      }
-#pragma unroll
-      for (int ks = 0; ks < D / M::K; ++ks) {
-        *(typename M::frag*)(Qs + pcol * RS + ks * M::K + M::KPL * g) = qc.f[ks];
-        *(typename M::frag*)(Gs + pcol * RS + ks * M::K + M::KPL * g) = gc.f[ks];
-      }
-    }
-    __syncthreads();
-
-    // ---- phase B: this wave's block of dV or dK over the tile's pairs
-#pragma unroll
-    for (int ks = 0; ks < QT / M::K; ++ks) {
-      const int ka = 32 * ks + 8 * g, kb = ka + 4;
-      typename M::frag af[MK2], bf[ND2];
-#pragma unroll
-      for (int x = 0; x < MK2; ++x) af[x] = tr_frag(Ab, PS, ka, kb, 16 * (mkb + x), lane);
-#pragma unroll
-      for (int y = 0; y < ND2; ++y) bf[y] = tr_frag(Bb, RS, ka, kb, 16 * (ndb + y), lane);
-#pragma unroll
-      for (int x = 0; x < MK2; ++x)
-#pragma unroll
-        for (int y = 0; y < ND2; ++y) acc[x][y] = M::mma(af[x], bf[y], acc[x][y]);
-    }
-  };
-
-  PairRows<E, D> ra, rb;
-  int e1 = idx(start + QT);
-  fetch(idx(start), ra);
-  for (int t0 = start; t0 < end; t0 += 2 * QT) {
-    ra.pin();
-    const int e2 = idx(t0 + 2 * QT);
-    fetch(e1, rb);
-    tile(ra);
-    if (t0 + QT >= end) break;
-    rb.pin();
-    e1 = idx(t0 + 3 * QT);
-    fetch(e2, ra);
-    tile(rb);
-  }
-
-  E* dv = (E*)a.dv;
-  if (dkw && !a.dk_leaf) return;
-#pragma unroll
-  for (int x = 0; x < MK2; ++x)
-#pragma unroll
-    for (int y = 0; y < ND2; ++y)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = 16 * (mkb + x) + 4 * g + r;
-        if (key < LB) {
-          const int64_t tok = (int64_t)beta * LB + key;
-          const int d = 16 * (ndb + y) + col;
-          const int64_t th = (((int64_t)bb * a.N + tok) * a.H + h) * D + d;
-          if (dkw) acc1f(a.dk_leaf + th, acc[x][y][r] * a.scale, a.first);
-          else if (a.dv32) acc1f(a.dv32 + th, acc[x][y][r], a.first);
-          else dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)acc[x][y][r];
-        }
-      }
-}
 
 template <typename E, int D, int LBP>
 static int bwd_smem_t() {
@@ -585,9 +270,9 @@ static int bwd_smem_t() {
 
 int leaf_bwd_smem(const Plan& P) {
   const int D = (int)P.D, LBP = padded_keys(P.geo.LB), ES = P.esize;
-  if (ES == 2) {  // the transposing-read kernel (BwdTrTile)
-    const int QT = LBP > 64 ? 64 : 128, RS = D + 16, PS = LBP + 16;
-    const int s = (2 * LBP * RS + 2 * QT * RS + 2 * QT * PS) * 2;
+  if (ES == 2) {  // the transposing-read kernel (BwdTrTile), with the plan's path rows
+    const int TR = P.path_rows;
+    const int s = bwd_tr_bytes(D, LBP, TR, bwd_tr_qt(D, LBP, TR));
     return s <= 160 * 1024 ? s : -1;
   }
   int s = 0;
@@ -637,12 +322,29 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
   a.dv32 = P.acc.dv32;
   a.first = P.acc.dv32 ? P.acc.first : 1;  // one launch: plain writes
   const unsigned grid = xcd_grid(P.BH, P.geo.NL);
-  constexpr int smem8 = BwdTrTile<D, LBP>::bytes;
+  if (P.path_rows) {
+    // the tree gradient along every pair's path (the plan allows it only for
+    // 16-bit inputs whose tile with the path rows fits the LDS)
+    a.delta = nullptr;
+    a.geo = P.geo;
+    a.NS = P.geo.NS;
+    a.maxhalf = 0.5f * P.p.max_logit;
+    a.inv_scale = 1.f / P.p.scale;
+    a.sum_hi = rec + P.rec.sum_hi;
+    a.dcp = (float*)(ws + P.bws.dcp);
+    if (P.acc.mean) {
+      a.mean = P.acc.mean;  // a chunk: dout . out over all samples, computed once
+    } else {
+      float* mean = (float*)(ws + P.bws.mean);
+      hipError_t e = launch_chunk_mean(P, g, (const float*)(rec + P.rec.out32), mean, st);
+      if (e != hipSuccess) return e;
+      a.mean = mean;
+    }
+    return launch_leaf_bwd_path(P, a, grid, st);
+  }
+  constexpr int smem8 = BwdTrTile<D, LBP, 0>::bytes;
   if constexpr (sizeof(E) == 2 && LBP >= 32 && smem8 <= 160 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_tr_kernel<E, D, LBP>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem8);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((leaf_bwd_tr_kernel<E, D, LBP>), dim3(grid), dim3(64 * BwdTrTile<D, LBP>::NW), smem8, st, a);
+    return launch_bwd_tr<E, D, LBP, 0>(a, grid, st);
   } else {
     const int smem = bwd_smem_t<E, D, LBP>();
     hipError_t e = hipFuncSetAttribute((const void*)leaf_bwd_kernel<E, D, LBP>,

@@ -254,9 +254,13 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   a.mode = P.p.tree_mode;
   // level lam holds the children of depth lam - 1 nodes: MFMA tiles in the
   // sampler below depth sample_dense (and, causal, the boundary nodes' children
-  // at every depth), in the tree backward below tree_dense (also transposed)
-  a.t_lam = P.tree_dense;
-  a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT ? G.T : (P.sample_dense > P.tree_dense ? P.sample_dense : P.tree_dense);
+  // at every depth), in the tree backward below tree_dense (also transposed),
+  // or with path rows every level's path children in the leaf backward (not
+  // transposed)
+  a.t_lam = P.path_rows ? 0 : P.tree_dense;
+  a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT || P.path_rows
+                   ? G.T
+                   : (P.sample_dense > P.tree_dense ? P.sample_dense : P.tree_dense);
   a.means = means;
   a.knodes = k;
   a.ksb = P.p.k_strides[0];

@@ -79,6 +79,7 @@ struct TreeArgs {
   // the first chunk, added by later ones), and so does the summary gradient
   float* dq32;
   int first;
+  const float* dcp;  // path rows: (BH, NL, T*b, D) per leaf block
 };
 
 template <typename E>
@@ -1056,19 +1057,6 @@ struct BandArgs {
 
 constexpr int kBandRows = 64;  // dC rows of one band's subtree (b = 2: 5 depths, b = 4: 2)
 
-template <typename E>
-__device__ __forceinline__ void ld8f(float* o, const E* p) {
-  if constexpr (sizeof(E) == 2) {
-    typedef __attribute__((ext_vector_type(8))) E e8;
-    const e8 v = *(const e8*)p;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (float)v[i];
-  } else {
-    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
-    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
-  }
-}
-
 template <typename E, int D, int kB>
 __global__ __launch_bounds__(256, 2) void tree_band_kernel(BandArgs a) {
   using M = Mfma<E>;
@@ -1313,12 +1301,103 @@ __global__ __launch_bounds__(256) void ref_band_boundary_kernel(TreeArgs a, int 
   }
 }
 
+// Path-row backward (the leaf backward added each pair's tree gradient to
+// its dq row and wrote each leaf block's gradient of its path's child
+// summaries, leaf_bwd_tr.h): dq[q] = the sum of the query's pair rows, in
+// slot order, one thread per (query, eight head dims); written to dq (E,
+// strided) or, for a chunk of a problem with many samples, to dq32.
+template <typename E>
+__global__ __launch_bounds__(256) void dq_rows_kernel(TreeArgs a, int64_t n8) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n8) return;
+  const int D = a.D;
+  const int64_t qh = e / (D / 8);
+  const int d0 = (int)(e - qh * (D / 8)) * 8;
+  const int64_t h = qh % a.H, bl = qh / a.H, l = bl % a.L, bb = bl / a.L;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  sum_rows8(acc, (const E*)a.dq_part + qh * a.S * D + d0, D, a.slot_count[qh]);
+  if (a.dq32) {
+    acc8f(a.dq32 + qh * D + d0, acc, a.first);
+    return;
+  }
+  E* o = (E*)a.dq + bb * a.qsb + l * a.qsl + h * a.qsh + d0;
+  if constexpr (sizeof(E) == 2) {
+    typedef __attribute__((ext_vector_type(8))) E e8;
+    e8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (E)acc[i];
+    *(e8*)o = v;
+  } else {
+    *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *(float4*)(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+// Path-row backward: dsum[row] for child j of the depth-d node n = the sum
+// over the leaf blocks u under n (u in [n b^(T-d), (n+1) b^(T-d)), in order of
+// lane) of dcp[u][d b + j]; rows padding a level are 0.  One wavefront per
+// (batch * head, summary row): lanes = DG groups of eight head dims x 64 / DG
+// block lanes (block lane i takes blocks lo + i, lo + i + 64 / DG, ...), then a
+// butterfly over the block lanes (a fixed order: deterministic).  dcp rows
+// are (BH, NL, T b, D) floats.  first = 0 (later chunks of a problem with many
+// samples) adds to dsum.
+template <int DG>
+__global__ __launch_bounds__(256) void path_dsum_kernel(const float* __restrict__ dcp, float* __restrict__ dsum,
+                                                        Geo G, int D, int64_t nrows, int first) {
+  const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (wv >= nrows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t bh = wv / G.NS;
+  const int row = (int)(wv - bh * G.NS);
+  int lam = 1;
+  while (lam < G.T && row >= G.off[lam + 1]) ++lam;
+  const int i = row - G.off[lam];
+  const int dg = lane % DG, bl = lane / DG;
+  constexpr int NBL = 64 / DG;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (i < G.pw[lam] && 8 * dg < D) {
+    const int d = lam - 1, j = i & (G.b - 1), n = i >> G.lb;
+    const int span = G.pw[G.T - d];
+    const int lo = n * span, hi = min(lo + span, G.NL);
+    const int nr = G.T * G.b;
+    const float* src = dcp + ((int64_t)bh * G.NL * nr + (int64_t)d * G.b + j) * D + 8 * dg;
+    for (int u = lo + bl; u < hi; u += NBL) {
+      const float* x = src + (int64_t)u * nr * D;
+      const float4 p0 = *(const float4*)x, p1 = *(const float4*)(x + 4);
+      acc[0] += p0.x; acc[1] += p0.y; acc[2] += p0.z; acc[3] += p0.w;
+      acc[4] += p1.x; acc[5] += p1.y; acc[6] += p1.z; acc[7] += p1.w;
+    }
+  }
+#pragma unroll
+  for (int o = DG; o < 64; o <<= 1)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] += __shfl_xor(acc[k], o, 64);
+  if (bl == 0 && 8 * dg < D) acc8f(dsum + ((int64_t)bh * G.NS + row) * D + 8 * dg, acc, first);
+}
+
 static int tree_smem(const Plan& P) {
   const int S = (int)P.S;
   // + the hoisted scan lanes (S <= 16): two floats and three ints each
   const int ch = chunk_cols((int)P.D);
   return kQueryTile * (ch + 4) * 4 + kQueryTile * (ch + 8) * P.esize + kQueryTile * S * 8 + kQueryTile * 4 +
          (S <= 8 ? kQueryTile * 8 * 20 : S <= 16 ? kQueryTile * 16 * 20 : 0);
+}
+
+// dk from the summary gradient (and the leaf part): once per problem, after
+// the last chunk of a problem with many samples.
+template <typename E>
+static hipError_t tree_adjoint(const Plan& P, const TreeArgs& a, bool chunk, hipStream_t st) {
+  if (chunk && !P.acc.last) return hipGetLastError();
+  const int D = a.D;
+  if (P.p.tree_mode == TA_TREE_NODEKEYS) {
+    const int64_t n = (int64_t)(P.geo.NL - 1) * D;
+    if (n > 0)
+      hipLaunchKernelGGL(nodekeys_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
+  } else {
+    const int64_t n = P.N * D / 8;
+    hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
 }
 
 template <typename E, int D>
@@ -1372,6 +1451,19 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
   a.dkl = P.geo.LB > 1 && P.p.tree_mode != TA_TREE_NODEKEYS;
 
   const int64_t nqh = P.B * P.L * P.H;
+  if (P.path_rows) {
+    // the leaf backward added the tree gradient: sum the pairs' dq rows and
+    // the leaf blocks' path rows under each node, then the key adjoint
+    a.dcp = (const float*)(ws + P.bws.dcp);
+    const int64_t n8 = nqh * (D / 8);
+    hipLaunchKernelGGL(dq_rows_kernel<E>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, a, n8);
+    const int64_t nrows = P.BH * P.geo.NS;
+    const dim3 grid((unsigned)((nrows + 3) / 4));
+    if (D <= 32) hipLaunchKernelGGL(path_dsum_kernel<4>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
+    else if (D <= 64) hipLaunchKernelGGL(path_dsum_kernel<8>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
+    else hipLaunchKernelGGL(path_dsum_kernel<16>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
+    return tree_adjoint<E>(P, a, chunk, st);
+  }
   int pw2 = 1;
   while (pw2 < P.S) pw2 <<= 1;
   hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
@@ -1444,16 +1536,7 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     hipLaunchKernelGGL(dsum_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        (const float*)a.dsum_part, a.dsum, n, P.qsplit, P.geo, D, a.nsd, a.first);
   }
-  if (chunk && !P.acc.last) return hipGetLastError();  // the key adjoint runs once, after the last chunk
-  if (P.p.tree_mode == TA_TREE_NODEKEYS) {
-    const int64_t n = (int64_t)(P.geo.NL - 1) * D;
-    if (n > 0)
-      hipLaunchKernelGGL(nodekeys_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
-  } else {
-    const int64_t n = P.N * D / 8;
-    hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
-  }
-  return hipGetLastError();
+  return tree_adjoint<E>(P, a, chunk, st);
 }
 
 template <typename E>
