@@ -67,9 +67,12 @@ def test_path_rows_layout():
     rec_d, fws_d, bws_d = _lib.byte_sizes(_problem(dense_cols=1024))
     assert rec_p == rec_d + out32 - sum_t and fws_p == fws_d
     assert bws_p < bws_d
-    # C4's shape (128-key blocks, head dim 128) keeps the dense levels
+    # C4's shape (128-key blocks, head dim 128, T*b = 20): 32 path rows
     c4 = dict(B=1, L=131072, N=131072, H=8, leaf_block=128, branching=2, causal=0)
-    assert _lib.byte_sizes(_problem(**c4)) == _lib.byte_sizes(_problem(dense_cols=1024, **c4))
+    assert _lib.byte_sizes(_problem(**c4))[2] < _lib.byte_sizes(_problem(dense_cols=1024, **c4))[2]
+    # T*b > 32 (b = 2 and 17 levels) keeps the dense levels and bands: no float output in the record
+    deep = dict(B=1, L=131072 * 2, N=131072 * 2, H=1, leaf_block=2, branching=2, causal=0)
+    assert _lib.byte_sizes(_problem(**deep))[0] == _lib.byte_sizes(_problem(dense_cols=1024, **deep))[0]
     f32 = dict(dtype=_lib.TA_F32, D=64)
     assert _lib.byte_sizes(_problem(**f32)) == _lib.byte_sizes(_problem(dense_cols=1024, **f32))
 

@@ -182,11 +182,9 @@ int make_plan(const ta_problem* p, Plan* P, bool chunk) {
   // blocks of two or more tokens, b = 2 or 4 with T*b <= 32, not the
   // reference causal mode, dense_cols at its default, and the leaf tile with
   // the path rows inside the LDS.  Otherwise the dense level tiles and bands.
-  // (128-key blocks with head dims of 96 or more already fill the 256 registers
-  // of the leaf tile's waves: those keep the dense levels)
   P->path_rows = 0;
   if (half && LB > 1 && (b == 2 || b == 4) && T >= 1 && T * b <= 32 && p->causal != TA_CAUSAL_REFERENCE &&
-      p->dense_cols == 0 && !(LB > 64 && D >= 96)) {
+      p->dense_cols == 0) {
     P->path_rows = T * b <= 16 ? 16 : 32;
     if (leaf_bwd_smem(*P) < 0) P->path_rows = 0;
   }

@@ -5,17 +5,14 @@
 
 namespace ta {
 
-// (make_plan gives no path rows to 128-key blocks with head dims of 96 or
-// more, nor to tiles that do not fit the LDS)
+// (make_plan gives no path rows to tiles that do not fit the LDS)
 template <typename E, int D, int LBP>
 static hipError_t path_lbp(const Plan& P, const LeafBwdArgs& a, unsigned grid, hipStream_t st) {
-  if constexpr (!(LBP > 64 && D >= 96)) {
-    if constexpr (BwdTrTile<D, LBP, 16>::bytes <= 160 * 1024) {
-      if (P.path_rows == 16) return launch_bwd_tr<E, D, LBP, 16>(a, grid, st);
-    }
-    if constexpr (BwdTrTile<D, LBP, 32>::bytes <= 160 * 1024) {
-      if (P.path_rows == 32) return launch_bwd_tr<E, D, LBP, 32>(a, grid, st);
-    }
+  if constexpr (BwdTrTile<D, LBP, 16>::bytes <= 160 * 1024) {
+    if (P.path_rows == 16) return launch_bwd_tr<E, D, LBP, 16>(a, grid, st);
+  }
+  if constexpr (BwdTrTile<D, LBP, 32>::bytes <= 160 * 1024) {
+    if (P.path_rows == 32) return launch_bwd_tr<E, D, LBP, 32>(a, grid, st);
   }
   return hipErrorInvalidValue;
 }

@@ -261,6 +261,95 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP, TR>::NW), (BwdTrTile<D, LBP
 #pragma unroll
   for (int i = 0; i < (NEW > 0 ? NEW : 1); ++i) cacc[i] = zero4();
 
+  // 128-key blocks (64-pair tiles): waves 0-3 run phase A of every tile and
+  // waves 4-7 phase B, so phase B of a tile overlaps phase A of the next, and
+  // no wave holds both the pair rows and the dV / dK accumulators.  Both
+  // groups pass the same two barriers per tile: X (phase B of the previous
+  // tile is done with the staging tiles) and Y (the tile is staged).
+  constexpr bool kSplit = LBP > 64;
+  static_assert(!kSplit || QT == 64, "split waves: 64-pair tiles");
+  if constexpr (kSplit) {
+    if (w >= 4) {
+      const int c4 = w - 4;  // keys 32 c4 .. 32 c4 + 31, every head dim, dV and dK
+      constexpr int NDT = D / 16, NEC = (NTE + 3) / 4;
+      f32x4 av[2][NDT], ak[2][NDT], cc[NEC > 0 ? NEC : 1];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NDT; ++y) av[x][y] = ak[x][y] = zero4();
+#pragma unroll
+      for (int i = 0; i < (NEC > 0 ? NEC : 1); ++i) cc[i] = zero4();
+      for (int t0 = start; t0 < end; t0 += QT) {
+        __syncthreads();  // X
+        __syncthreads();  // Y
+#pragma unroll
+        for (int ks = 0; ks < QT / M::K; ++ks) {
+          const int ka = 32 * ks + 8 * g, kb = ka + 4;
+          typename M::frag pv[2], zk[2];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            pv[x] = tr_frag(Ps, PS, ka, kb, 16 * (2 * c4 + x), lane);
+            zk[x] = tr_frag(Zs, ZS, ka, kb, 16 * (2 * c4 + x), lane);
+          }
+#pragma unroll
+          for (int y = 0; y < NDT; ++y) {
+            const typename M::frag bg = tr_frag(Gs, RS, ka, kb, 16 * y, lane);
+            const typename M::frag bq = tr_frag(Qs, RS, ka, kb, 16 * y, lane);
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              av[x][y] = M::mma(pv[x], bg, av[x][y]);
+              ak[x][y] = M::mma(zk[x], bq, ak[x][y]);
+            }
+          }
+          if constexpr (TR > 0) {
+#pragma unroll
+            for (int i = 0; i < NEC; ++i) {
+              const int t = c4 + 4 * i;
+              if (NTE % 4 == 0 || t < NTE) {
+                const int rt = t / NDT, dt = t - rt * NDT;
+                cc[i] = M::mma(tr_frag(Zs, ZS, ka, kb, LBP + 16 * rt, lane), tr_frag(Qs, RS, ka, kb, 16 * dt, lane),
+                               cc[i]);
+              }
+            }
+          }
+        }
+      }
+      if constexpr (TR > 0) {  // this block's path-row gradient (zero for a block without pairs)
+        float* dc = a.dcp + ((int64_t)bh * a.NL + beta) * nrow * D;
+#pragma unroll
+        for (int i = 0; i < NEC; ++i) {
+          const int t = c4 + 4 * i;
+          if (NTE % 4 == 0 || t < NTE) {
+            const int rt = t / NDT, dt = t - rt * NDT;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int e = 16 * rt + 4 * g + r;
+              if (e < nrow) dc[(int64_t)e * D + 16 * dt + col] = cc[i][r] * a.scale;
+            }
+          }
+        }
+      }
+      E* dv = (E*)a.dv;
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NDT; ++y)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = 16 * (2 * c4 + x) + 4 * g + r;
+            if (key < LB) {
+              const int64_t tok = (int64_t)beta * LB + key;
+              const int d = 16 * y + col;
+              const int64_t th = (((int64_t)bb * a.N + tok) * a.H + h) * D + d;
+              if (a.dk_leaf) acc1f(a.dk_leaf + th, ak[x][y][r] * a.scale, a.first);
+              if (a.dv32) acc1f(a.dv32 + th, av[x][y][r], a.first);
+              else dv[bb * a.vsb + tok * a.vsl + h * a.vsh + d] = (E)av[x][y][r];
+            }
+          }
+      return;
+    }
+  }
+
   // Software pipeline over QT-pair tiles with two register sets: a tile
   // first waits for its own set (loaded one tile earlier), then issues the
   // loads of the next tile into the other set and reads the pair index of the
@@ -446,7 +535,8 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP, TR>::NW), (BwdTrTile<D, LBP
     __syncthreads();
 
     // ---- phase B: this wave's block of dV or dK over the tile's pairs, and
-    // its tiles of the path rows' dC
+    // its tiles of the path rows' dC (split waves: waves 4-7, above)
+    if constexpr (!kSplit) {
 #pragma unroll
     for (int ks = 0; ks < QT / M::K; ++ks) {
       const int ka = 32 * ks + 8 * g, kb = ka + 4;
@@ -471,6 +561,7 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP, TR>::NW), (BwdTrTile<D, LBP
         }
       }
     }
+    }  // !kSplit
   };
 
   PairRows<E, D> ra, rb;
@@ -487,6 +578,7 @@ __global__ __launch_bounds__((64 * BwdTrTile<D, LBP, TR>::NW), (BwdTrTile<D, LBP
     fetch(e2, ra);
     tile(rb);
   }
+  if constexpr (kSplit) return;  // waves 4-7 write the block's gradients
 
   if constexpr (TR > 0) {  // this block's path-row gradient (zero for a block without pairs)
     float* dc = a.dcp + ((int64_t)bh * a.NL + beta) * nrow * D;
