@@ -80,12 +80,17 @@ def parse():
 
 
 def tree_units(B, L, H, D, e, b, LB, S):
-    """Algorithmic bytes / FLOPs per launch of each phase (uniforms generated in-kernel)."""
+    """Algorithmic bytes / FLOPs per launch of each phase (uniforms generated in-kernel).
+
+    With 16-bit inputs, LB > 1, b = 2 or 4 and T*b <= 32 the leaf backward also computes the tree
+    gradient along every sample's path (per sample and depth the b child logits, their share of
+    dq and of the child summaries' gradient: 6 b D FLOPs), which the leaf_backward phase then counts."""
     NL = L // LB
     T = round(math.log(NL, b))
     NS = b * (NL - 1) // (b - 1)
     BLHD, BLHS = B * L * H * D, B * L * H * S
     sums = NS * B * H * D * e
+    path = e == 2 and LB > 1 and b in (2, 4) and T * b <= 32
     return dict(
         T=T,
         NS=NS,
@@ -93,7 +98,7 @@ def tree_units(B, L, H, D, e, b, LB, S):
         sample_bytes=BLHD * e + sums + BLHS * 12,
         sample_flops=BLHS * T * b * 2 * D,
         leaf_fwd_flops=BLHS * 4 * LB * D,
-        leaf_bwd_flops=BLHS * 10 * LB * D,
+        leaf_bwd_flops=BLHS * 10 * LB * D + (BLHS * 6 * T * b * D if path else 0),
         fwd_bytes=4 * BLHD * e + BLHS * 8 + 2 * sums,
         bwd_bytes=8 * BLHD * e + BLHS * 8 + 2 * sums,
     )
