@@ -935,18 +935,22 @@ __global__ __launch_bounds__(256) void dsum_reduce_kernel(const float* __restric
 }
 
 // dk[b, t, h, :] = dk_leaf + sum over the summaries that include token t.
-// One thread per (token, 8 dims): one 16-byte store for 16-bit outputs (the
-// entry points require 16-byte aligned dk and strides in multiples of 8);
-// grid (ceil(N*D/8/256), BH).
+// The summary part depends only on t's leaf block, so one thread per (leaf
+// block, run of up to kAdjTok of its tokens, 8 dims) sums it once (T summary
+// rows) and writes the run's tokens: one 16-byte store each for 16-bit
+// outputs (the entry points require 16-byte aligned dk and strides in
+// multiples of 8); grid (ceil(NL * runs * D/8 / 256), BH).
+constexpr int kAdjTok = 16;
 template <typename E>
-__global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
+__global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a, int runs) {
   const Geo& G = a.geo;
   const int D = a.D;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)a.N * D / 8) return;
+  const int64_t rest = e / (D / 8);
+  const int d0 = (int)(e - rest * (D / 8)) * 8;
+  const int beta = (int)(rest / runs), run = (int)(rest - (int64_t)beta * runs);
+  if (beta >= G.NL) return;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
-  const int t = (int)(e / (D / 8)), d0 = (int)(e - (int64_t)t * (D / 8)) * 8;
-  const int beta = t / G.LB;
   const float* ds = a.dsum + (int64_t)bh * G.NS * D + d0;
   float acc[8];
 #pragma unroll
@@ -980,25 +984,30 @@ __global__ __launch_bounds__(256) void pool_adjoint_kernel(TreeArgs a) {
     }
   }
   const float inv = 1.f / (float)G.LB;
-  const int64_t th = ((int64_t)bb * a.N + t) * a.H + h;
-  float4 l0 = make_float4(0.f, 0.f, 0.f, 0.f), l1 = l0;
-  if (a.dkl) {
-    const float4* lk = (const float4*)(a.dk_leaf + th * D + d0);
-    l0 = lk[0];
-    l1 = lk[1];
-  }
-  const float r[8] = {l0.x + acc[0] * inv, l0.y + acc[1] * inv, l0.z + acc[2] * inv, l0.w + acc[3] * inv,
-                      l1.x + acc[4] * inv, l1.y + acc[5] * inv, l1.z + acc[6] * inv, l1.w + acc[7] * inv};
-  E* o = (E*)a.dk + bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d0;
-  if constexpr (sizeof(E) == 2) {
-    typedef __attribute__((ext_vector_type(8))) E e8;
-    e8 v;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (E)r[i];
-    *(e8*)o = v;
-  } else {
-    *(float4*)o = make_float4(r[0], r[1], r[2], r[3]);
-    *(float4*)(o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+  for (int i = 0; i < 8; ++i) acc[i] *= inv;
+  const int t0 = beta * G.LB + run * kAdjTok, t1 = min(t0 + kAdjTok, (beta + 1) * G.LB);
+  for (int t = t0; t < t1; ++t) {
+    const int64_t th = ((int64_t)bb * a.N + t) * a.H + h;
+    float4 l0 = make_float4(0.f, 0.f, 0.f, 0.f), l1 = l0;
+    if (a.dkl) {
+      const float4* lk = (const float4*)(a.dk_leaf + th * D + d0);
+      l0 = lk[0];
+      l1 = lk[1];
+    }
+    const float r[8] = {l0.x + acc[0], l0.y + acc[1], l0.z + acc[2], l0.w + acc[3],
+                        l1.x + acc[4], l1.y + acc[5], l1.z + acc[6], l1.w + acc[7]};
+    E* o = (E*)a.dk + bb * a.ksb + (int64_t)t * a.ksl + h * a.ksh + d0;
+    if constexpr (sizeof(E) == 2) {
+      typedef __attribute__((ext_vector_type(8))) E e8;
+      e8 v;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (E)r[i];
+      *(e8*)o = v;
+    } else {
+      *(float4*)o = make_float4(r[0], r[1], r[2], r[3]);
+      *(float4*)(o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+    }
   }
 }
 
@@ -1394,8 +1403,9 @@ static hipError_t tree_adjoint(const Plan& P, const TreeArgs& a, bool chunk, hip
     if (n > 0)
       hipLaunchKernelGGL(nodekeys_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
   } else {
-    const int64_t n = P.N * D / 8;
-    hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a);
+    const int runs = (P.geo.LB + kAdjTok - 1) / kAdjTok;
+    const int64_t n = (int64_t)P.geo.NL * runs * (D / 8);
+    hipLaunchKernelGGL(pool_adjoint_kernel<E>, dim3((unsigned)((n + 255) / 256), P.BH), dim3(256), 0, st, a, runs);
   }
   return hipGetLastError();
 }
