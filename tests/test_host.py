@@ -58,14 +58,14 @@ def test_struct_layout_and_sizes():
 
 def test_path_rows_layout():
     """16-bit problems with b = 2 or 4 and T*b <= 32 take the tree gradient along each pair's
-    path in the leaf backward: the record keeps the float output (dout . out in the backward)
+    path in the leaf backward: the record keeps a copy of the output (dout . out in the backward)
     and the backward workspace drops the dense G^T tiles; dense_cols > 0 keeps the dense
     levels, float inputs and one-token leaves always do."""
-    out32 = 2 * 16384 * 16 * 128 * 4
+    out_e = 2 * 16384 * 16 * 128 * 2             # a bf16 copy of the output
     sum_t = 32 * (32 + 32 + 64 + 256) * 128 * 2  # the dense backward's transposed summaries
     rec_p, fws_p, bws_p = _lib.byte_sizes(_problem())
     rec_d, fws_d, bws_d = _lib.byte_sizes(_problem(dense_cols=1024))
-    assert rec_p == rec_d + out32 - sum_t and fws_p == fws_d
+    assert rec_p == rec_d + out_e - sum_t and fws_p == fws_d
     assert bws_p < bws_d
     # C4's shape (128-key blocks, head dim 128, T*b = 20): 32 path rows
     c4 = dict(B=1, L=131072, N=131072, H=8, leaf_block=128, branching=2, causal=0)
@@ -106,8 +106,8 @@ def test_many_samples_run_in_chunks():
     sample's leaf block and the float output; workspaces are reused chunk after chunk."""
     one = _lib.byte_sizes(_problem(num_samples=64))
     two = _lib.byte_sizes(_problem(num_samples=128))
-    out32 = 2 * 16384 * 16 * 128 * 4    # the float output, kept once per problem
-    assert two[0] > 2 * one[0] - out32  # two chunk records + leaves + float output
+    out_e = 2 * 16384 * 16 * 128 * 2    # the single-chunk record's copy of the output
+    assert two[0] > 2 * one[0] - out_e  # two chunk records + leaves + float output
     assert two[1] == one[1]             # chunks of 64: the same forward workspace
     assert two[2] > one[2]              # + float accumulators
     lo = _lib.record_offset(_problem(num_samples=128), _lib.TA_REC_LEAVES)

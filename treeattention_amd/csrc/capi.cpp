@@ -214,7 +214,7 @@ int make_plan(const ta_problem* p, Plan* P, bool chunk) {
   P->rec.sort_keys = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
   P->rec.sort_vals = r.take(P->bucket_sort ? 2 * BLHS * 4 : 0);
   P->rec.sort_hist = r.take(P->bucket_sort ? 256 * ((BLHS + 2047) / 2048 + 1) * 4 : 0);
-  P->rec.out32 = r.take(pr && !chunk ? B * L * H * D * 4 : 0);
+  P->rec.out_e = r.take(pr && !chunk ? B * L * H * D * es : 0);
   P->rec.total = r.at;
   const bool lb1 = LB == 1;  // leaf stage: a value gather, no pair rows
   Carver f;
@@ -394,7 +394,7 @@ int backward_chunks(const ta_problem* p, const void* q, const void* k, const voi
   acc.dsum = (float*)(ws + C.bws_dsum);
   acc.mean = (const float*)(ws + C.bws_mean);
   const Plan& P0 = C.P[0];
-  hipError_t e = launch_chunk_mean(P0, grad_out, (const float*)(rec + C.rec_out32), (float*)(ws + C.bws_mean), st);
+  hipError_t e = launch_chunk_mean(P0, grad_out, rec + C.rec_out32, false, (float*)(ws + C.bws_mean), st);
   if (e != hipSuccess) return launch_status(e, "chunk_mean");
   for (int g = 0; g < C.n; ++g) {
     Plan P = C.P[g];

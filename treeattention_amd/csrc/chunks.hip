@@ -52,12 +52,13 @@ hipError_t launch_chunk_merge(const Plan& P, const ChunkRecs& R, float* weights,
   return hipGetLastError();
 }
 
-// mean[b, l, h] = dout[b, l, h, :] . out32[b, l, h, :]; a group of DG lanes
-// per row (DG = D / 8 rounded up to a power of two), eight dims per lane in
-// 16-byte loads, then a butterfly over the group (a fixed order).
-template <typename E, int DG>
+// mean[b, l, h] = dout[b, l, h, :] . out[b, l, h, :] (out: the forward's
+// (B, L, H, D) rows, float or E); a group of DG lanes per row (DG = D / 8
+// rounded up to a power of two), eight dims per lane in 16-byte loads, then a
+// butterfly over the group (a fixed order).
+template <typename E, typename O, int DG>
 __global__ __launch_bounds__(256) void chunk_mean_kernel(const E* __restrict__ g, int64_t gsb, int64_t gsl,
-                                                         int64_t gsh, const float* __restrict__ out32,
+                                                         int64_t gsh, const O* __restrict__ out,
                                                          float* __restrict__ mean, int L, int H, int D, int64_t nqh) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t qh = gid / DG;
@@ -65,39 +66,44 @@ __global__ __launch_bounds__(256) void chunk_mean_kernel(const E* __restrict__ g
   float s = 0.f;
   if (qh < nqh && 8 * dg < D) {
     const int64_t h = qh % H, bl = qh / H, l = bl % L, bb = bl / L;
-    float gv[8];
+    float gv[8], ov[8];
     ld8f(gv, g + bb * gsb + l * gsl + h * gsh + 8 * dg);
-    const float* o = out32 + qh * D + 8 * dg;
-    const float4 o0 = *(const float4*)o, o1 = *(const float4*)(o + 4);
-    s = gv[0] * o0.x + gv[1] * o0.y + gv[2] * o0.z + gv[3] * o0.w + gv[4] * o1.x + gv[5] * o1.y + gv[6] * o1.z +
-        gv[7] * o1.w;
+    ld8f(ov, out + qh * D + 8 * dg);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += gv[i] * ov[i];
   }
 #pragma unroll
   for (int m = 1; m < DG; m <<= 1) s += __shfl_xor(s, m, 64);
   if (qh < nqh && dg == 0) mean[qh] = s;
 }
 
-template <typename E, int DG>
-static void mean_launch(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
+template <typename E, typename O, int DG>
+static void mean_launch(const Plan& P, const void* g, const O* out, float* mean, hipStream_t st) {
   const int64_t nqh = P.B * P.L * P.H;
   const dim3 grid((unsigned)((nqh * DG + 255) / 256));
   const int64_t* gs = P.p.g_strides;
-  hipLaunchKernelGGL((chunk_mean_kernel<E, DG>), grid, dim3(256), 0, st, (const E*)g, gs[0], gs[1], gs[2], out32,
+  hipLaunchKernelGGL((chunk_mean_kernel<E, O, DG>), grid, dim3(256), 0, st, (const E*)g, gs[0], gs[1], gs[2], out,
                      mean, (int)P.L, (int)P.H, (int)P.D, nqh);
 }
 
 template <typename E>
-static void mean_d(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
-  if (P.D <= 32) mean_launch<E, 4>(P, g, out32, mean, st);
-  else if (P.D <= 64) mean_launch<E, 8>(P, g, out32, mean, st);
-  else mean_launch<E, 16>(P, g, out32, mean, st);
+static void mean_d(const Plan& P, const void* g, const void* out, bool out_e, float* mean, hipStream_t st) {
+  if (out_e) {
+    if (P.D <= 32) mean_launch<E, E, 4>(P, g, (const E*)out, mean, st);
+    else if (P.D <= 64) mean_launch<E, E, 8>(P, g, (const E*)out, mean, st);
+    else mean_launch<E, E, 16>(P, g, (const E*)out, mean, st);
+  } else {
+    if (P.D <= 32) mean_launch<E, float, 4>(P, g, (const float*)out, mean, st);
+    else if (P.D <= 64) mean_launch<E, float, 8>(P, g, (const float*)out, mean, st);
+    else mean_launch<E, float, 16>(P, g, (const float*)out, mean, st);
+  }
 }
 
-hipError_t launch_chunk_mean(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st) {
+hipError_t launch_chunk_mean(const Plan& P, const void* g, const void* out, bool out_e, float* mean, hipStream_t st) {
   switch (P.p.dtype) {
-    case TA_F32: mean_d<float>(P, g, out32, mean, st); break;
-    case TA_BF16: mean_d<bf16>(P, g, out32, mean, st); break;
-    default: mean_d<f16>(P, g, out32, mean, st);
+    case TA_F32: mean_d<float>(P, g, out, out_e, mean, st); break;
+    case TA_BF16: mean_d<bf16>(P, g, out, out_e, mean, st); break;
+    default: mean_d<f16>(P, g, out, out_e, mean, st);
   }
   return hipGetLastError();
 }

@@ -578,7 +578,7 @@ struct RecordLayout {
   int64_t sort_keys;   // uint32 (2, B, L, H, S): bucketing by sort, key double buffer
   int64_t sort_vals;   // int (2, B, L, H, S): bucketing by sort, value double buffer
   int64_t sort_hist;   // int (256, tiles of 2048 keys + 1): the sort's per-tile digit counts, digit totals
-  int64_t out32;       // float (B, L, H, D): the forward output before rounding (path rows, one chunk)
+  int64_t out_e;       // E (B, L, H, D): a copy of the forward output (path rows, one chunk)
   int64_t total;
 };
 

@@ -142,7 +142,8 @@ struct ChunkRecs {
 };
 hipError_t launch_chunk_merge(const Plan& P, const ChunkRecs& R, float* weights, int* leaf_all, hipStream_t st);
 // mean[b,l,h] = dout . out32 over the head dim
-hipError_t launch_chunk_mean(const Plan& P, const void* g, const float* out32, float* mean, hipStream_t st);
+// out: (B, L, H, D) rows of the forward output, float or (out_e) the input type
+hipError_t launch_chunk_mean(const Plan& P, const void* g, const void* out, bool out_e, float* mean, hipStream_t st);
 // dst (E, strides st3 (batch, row, head)) = src (float (B, R, H, D) contiguous)
 hipError_t launch_cast_rows(int dtype, const float* src, void* dst, const int64_t* st3, int64_t B, int64_t R,
                             int64_t H, int64_t D, hipStream_t st);

@@ -336,7 +336,7 @@ static hipError_t leaf_bwd_impl(const Plan& P, const void* q, const void* k, con
       a.mean = P.acc.mean;  // a chunk: dout . out over all samples, computed once
     } else {
       float* mean = (float*)(ws + P.bws.mean);
-      hipError_t e = launch_chunk_mean(P, g, (const float*)(rec + P.rec.out32), mean, st);
+      hipError_t e = launch_chunk_mean(P, g, rec + P.rec.out_e, true, mean, st);
       if (e != hipSuccess) return e;
       a.mean = mean;
     }

@@ -315,14 +315,15 @@ __global__ __launch_bounds__(256, 2) void leaf_fwd16_kernel(LeafFwdArgs a) {
 // out[b,l,h,:] = sum over the query's distinct leaf blocks of the partial rows,
 // for the L * nbh queries of the launch's (batch, head) group, position-major
 // (consecutive threads write consecutive heads of one position).  With out32
-// the sum also goes to the float (B, L, H, D) rows: for a chunk of a problem
-// with many samples instead of out (written by the first chunk, added by later
-// ones, keep = 0), for the path-row backward beside out (keep = 1).
+// (a chunk of a problem with many samples) the sum goes to the float
+// (B, L, H, D) rows instead: written by the first chunk, added by later ones.
+// With oe (16-bit, the path-row backward's dout . out) out is also copied to
+// the contiguous (B, L, H, D) rows oe.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ partial, const int* __restrict__ slot_count,
                                                       E* __restrict__ out, int L, int H, int S, int bh0, int nbh,
                                                       int64_t osb, int64_t osl, int64_t osh, float* __restrict__ out32,
-                                                      int first, int keep) {
+                                                      int first, E* __restrict__ oe) {
   constexpr int TPQ = D / 8;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gid / TPQ;
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ part
   sum_rows8(acc, partial + (bhl * L + l) * S * D + 8 * part, D, slot_count[qh]);
   if (out32) {
     acc8f(out32 + qh * D + 8 * part, acc, first);
-    if (!keep) return;
+    return;
   }
   E* o = out + bb * osb + l * osl + h * osh + 8 * part;
   if constexpr (sizeof(E) == 2) {
@@ -344,6 +345,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const E* __restrict__ part
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (E)acc[i];
     *(e8*)o = v;
+    if (oe) *(e8*)(oe + qh * D + 8 * part) = v;
   } else {
     *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
     *(float4*)(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
@@ -413,13 +415,12 @@ static hipError_t leaf_fwd_impl(const Plan& P, const void* q, const void* k, con
   const int64_t nrows = (int64_t)nbh * P.L;
   const int64_t nthr = nrows * (D / 8);
   // a chunk adds into the problem's float output; with path rows the record
-  // keeps the float output too (the backward's dout . out)
-  float* o32 = P.acc.out32 ? P.acc.out32 : P.path_rows ? (float*)(rec + P.rec.out32) : nullptr;
-  const int first = P.acc.out32 ? P.acc.first : 1;
+  // keeps a copy of the output (the backward's dout . out)
+  E* oe = !P.acc.out32 && P.path_rows ? (E*)(rec + P.rec.out_e) : nullptr;
   hipLaunchKernelGGL((combine_kernel<E, D>), dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st,
                      (const E*)a.partial, (const int*)(rec + P.rec.slot_count), (E*)out, (int)P.L, (int)P.H,
-                     (int)P.S, bh0, nbh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2], o32, first,
-                     P.acc.out32 ? 0 : 1);
+                     (int)P.S, bh0, nbh, P.p.o_strides[0], P.p.o_strides[1], P.p.o_strides[2], P.acc.out32,
+                     P.acc.first, oe);
   return hipGetLastError();
 }
 
