@@ -72,8 +72,11 @@ typedef struct ta_problem {
   int32_t causal;        /* TA_CAUSAL_* */
   int32_t dtype;         /* TA_F32 / TA_BF16 / TA_F16 */
   int32_t dense_cols;    /* tree levels with at most this many children run as dense level
-                            tiles, wider ones per sampled path (0: the library's defaults);
-                            changes no result beyond rounding, for tuning and tests */
+                            tiles, wider ones per sampled path (0: the library's defaults,
+                            which for 16-bit inputs with b = 2 or 4, leaf_block >= 2 and
+                            T*b <= 32 take the backward's tree part along the sampled paths
+                            in the leaf backward); changes no result beyond rounding, for
+                            tuning and tests */
   float scale;           /* leaf-block softmax scale */
   float max_logit;       /* child logits are clamped to +-max_logit/2 (binary compat trees:
                             the left/right logit to +-max_logit, _autograd.py:202) */
@@ -234,9 +237,13 @@ int ta_forward_replay(const ta_problem* p, const void* q, const void* k, const v
                       void* workspace, void* stream);
 
 /* Backward, leaf-block part: dv (complete), the leaf contribution to dk and
- * per-pair dq and dout.o into `workspace`.  Replaces
- * scatter_weighted_grad_v_forward (treeattn_cuda.cpp:290) and the value side
- * of prepare_non_causal_backward (:176), without atomics. */
+ * per-pair dq and dout.o into `workspace`.  For 16-bit inputs with b = 2 or
+ * 4, leaf_block >= 2, T*b <= 32 and dense_cols = 0 it also takes the tree
+ * gradient along every pair's sampled path (the pair's dq row then holds both
+ * parts, and each leaf block's gradient of its path's child summaries goes to
+ * `workspace`).  Replaces scatter_weighted_grad_v_forward
+ * (treeattn_cuda.cpp:290) and the value side of prepare_non_causal_backward
+ * (:176), without atomics. */
 int ta_leaf_backward(const ta_problem* p, const void* q, const void* k, const void* v,
                      const void* grad_out, const void* record, void* dv, void* workspace, void* stream);
 

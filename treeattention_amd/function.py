@@ -57,8 +57,10 @@ class TreeOptions:
     * ``layout``: ``"bshd"`` (B, L, H, D) or ``"lbhd"`` (L, B, H, D).
     * ``dense_cols``: tree levels with at most this many children are
       evaluated as dense level tiles, wider ones per sampled path (0: the
-      library's defaults); for tuning and tests, results change only by
-      rounding.
+      library's defaults, under which 16-bit inputs with b = 2 or 4,
+      ``leaf_block >= 2`` and ``T*b <= 32`` take the backward's tree part
+      along the sampled paths inside the leaf backward); for tuning and
+      tests, results change only by rounding.
     """
 
     num_samples: int
