@@ -188,12 +188,20 @@ int make_plan(const ta_problem* p, Plan* P, bool chunk) {
     P->path_rows = T * b <= 16 ? 16 : 32;
     if (leaf_bwd_smem(*P) < 0) P->path_rows = 0;
   }
-  const bool pr = P->path_rows > 0;
+  // One-token leaves (the reference's binary tree), 16-bit, not the reference
+  // causal mode, dense_cols at its default: the tree gradient along the paths
+  // per subtree of 2^g leaves (leaf_path1.hip), up to 16 depths above them.
+  P->leaf_path = 0;
+  if (half && LB == 1 && b == 2 && T >= 1 && p->causal != TA_CAUSAL_REFERENCE && p->dense_cols == 0) {
+    const int g = leaf_path1_depth(T);
+    if (2 * (T - g) <= leaf_path1_top_rows() && leaf_path1_smem((int)D) <= 160 * 1024) P->leaf_path = g;
+  }
+  const bool pr = P->path_rows > 0, lp = P->leaf_path > 0;
   Carver r;
   P->rec.summaries = r.take(P->BH * G.NS * D * 4);
   P->rec.sum_hi = r.take(half ? P->BH * G.NS * D * es : 0);
   P->rec.sum_lo = r.take(half ? P->BH * G.NS * D * es : 0);
-  P->rec.sum_t = r.take(pr ? 0 : P->BH * G.NS * D * es);  // the dense backward's transposed copy
+  P->rec.sum_t = r.take(pr || lp ? 0 : P->BH * G.NS * D * es);  // the dense backward's transposed copy
   P->rec.means = r.take(p->tree_mode == TA_TREE_NODEKEYS ? 0 : P->BH * NL * D * 4);
   P->rec.segs = r.take(p->tree_mode == TA_TREE_NODEKEYS || NL < 128 ? 0 : P->BH * (NL / 64 + NL / 4096) * D * 4);
   P->rec.leaf = r.take(BLHS * 4);
@@ -222,15 +230,16 @@ int make_plan(const ta_problem* p, Plan* P, bool chunk) {
   P->fws.total = f.at;
   Carver w;
   P->bws.delta = w.take(pr ? 0 : BLHS * 4);
-  P->bws.dq_part = w.take(!lb1 || P->tree_dense < T ? BLHS * D * es : 0);
+  P->bws.dq_part = w.take(!lb1 || lp || P->tree_dense < T ? BLHS * D * es : 0);
   P->bws.dlogp = w.take(pr ? 0 : BLHS * 4);
   P->bws.dk_leaf = w.take(p->tree_mode == TA_TREE_NODEKEYS || lb1 ? 0 : B * N * H * D * 4);
-  P->bws.gt = w.take(pr ? 0 : P->BH * NSd * P->Lp * es);
-  P->bws.qt = w.take(pr ? 0 : P->BH * D * P->Lp * es);
-  P->bws.dsum_part = w.take(pr ? 0 : qsplit * P->BH * NSd * D * 4);
+  P->bws.gt = w.take(pr || lp ? 0 : P->BH * NSd * P->Lp * es);
+  P->bws.qt = w.take(pr || lp ? 0 : P->BH * D * P->Lp * es);
+  P->bws.dsum_part = w.take(pr || lp ? 0 : qsplit * P->BH * NSd * D * 4);
   P->bws.dsum = w.take(P->BH * G.NS * D * 4);
   P->bws.mean = w.take(pr ? B * L * H * 4 : 0);
-  P->bws.dcp = w.take(pr ? P->BH * NL * T * b * D * 4 : 0);
+  P->bws.dcp = w.take(pr ? P->BH * NL * T * b * D * 4
+                         : lp ? P->BH * (NL >> P->leaf_path) * leaf_path1_top_rows() * D * 4 : 0);
   const bool rc = p->causal == TA_CAUSAL_REFERENCE;
   P->bws.rc_coef = w.take(rc ? B * L * H * T * 4 : 0);
   P->bws.rc_rho = w.take(rc ? B * L * H * T * 4 : 0);

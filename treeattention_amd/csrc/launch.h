@@ -35,6 +35,8 @@ struct Plan {
   int sample_dense; // the sampler's level tiles cover depths < sample_dense; deeper levels are sparse
   int tree_dense;   // the backward's dense G tiles cover depths < tree_dense; deeper ones run in bands
   int bucket_sort;  // many leaf blocks: bucketing by a radix sort of (batch * head, leaf block) keys
+  int leaf_path;    // > 0 (one-token leaves): the tree gradient along the paths per subtree of
+                   // 2^leaf_path leaves (leaf_path1.hip) instead of dense levels and bands
   int path_rows;    // > 0: the leaf backward adds the tree gradient along each pair's path (T*b rows,
                    // padded to 16 or 32); the tree backward only sums rows and blocks
   int64_t s0, s_total;  // this plan's samples are s0 .. s0 + S - 1 of s_total (uniform / path indices)
@@ -159,6 +161,12 @@ hipError_t launch_gather_bwd(const Plan& P, const void* v, const void* g, void* 
 int leaf_fwd_smem(const Plan& P);
 int ref_sample_smem(const Plan& P);
 int leaf_bwd_smem(const Plan& P);
+// leaf_path1.hip
+int leaf_path1_depth(int T);
+int leaf_path1_top_rows();
+int leaf_path1_smem(int D);
+hipError_t launch_leaf_path1(const Plan& P, const void* q, const char* rec, char* ws, float* dsum, int first,
+                             hipStream_t st);
 
 inline int padded_keys(int LB) { return LB <= 32 ? 32 : (LB <= 64 ? 64 : 128); }
 

@@ -257,8 +257,8 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   // at every depth), in the tree backward below tree_dense (also transposed),
   // or with path rows every level's path children in the leaf backward (not
   // transposed)
-  a.t_lam = P.path_rows ? 0 : P.tree_dense;
-  a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT || P.path_rows
+  a.t_lam = P.path_rows || P.leaf_path ? 0 : P.tree_dense;
+  a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT || P.path_rows || P.leaf_path
                    ? G.T
                    : (P.sample_dense > P.tree_dense ? P.sample_dense : P.tree_dense);
   a.means = means;

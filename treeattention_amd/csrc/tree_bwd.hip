@@ -1350,9 +1350,13 @@ __global__ __launch_bounds__(256) void dq_rows_kernel(TreeArgs a, int64_t n8) {
 // butterfly over the block lanes (a fixed order: deterministic).  dcp rows
 // are (BH, NL, T b, D) floats.  first = 0 (later chunks of a problem with many
 // samples) adds to dsum.
+// (Also the one-token leaves' per-subtree root-path rows, leaf_path1.hip: G
+// then describes the tree above the subtrees -- T = depths above them, NL =
+// subtrees, NS = the rows of those levels -- nr = rows per subtree and ns the
+// summary-gradient rows per (batch, head).)
 template <int DG>
 __global__ __launch_bounds__(256) void path_dsum_kernel(const float* __restrict__ dcp, float* __restrict__ dsum,
-                                                        Geo G, int D, int64_t nrows, int first) {
+                                                        Geo G, int D, int64_t nrows, int first, int nr, int ns) {
   const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (wv >= nrows) return;
   const int lane = threadIdx.x & 63;
@@ -1368,7 +1372,6 @@ __global__ __launch_bounds__(256) void path_dsum_kernel(const float* __restrict_
     const int d = lam - 1, j = i & (G.b - 1), n = i >> G.lb;
     const int span = G.pw[G.T - d];
     const int lo = n * span, hi = min(lo + span, G.NL);
-    const int nr = G.T * G.b;
     const float* src = dcp + ((int64_t)bh * G.NL * nr + (int64_t)d * G.b + j) * D + 8 * dg;
     for (int u = lo + bl; u < hi; u += NBL) {
       const float* x = src + (int64_t)u * nr * D;
@@ -1381,7 +1384,7 @@ __global__ __launch_bounds__(256) void path_dsum_kernel(const float* __restrict_
   for (int o = DG; o < 64; o <<= 1)
 #pragma unroll
     for (int k = 0; k < 8; ++k) acc[k] += __shfl_xor(acc[k], o, 64);
-  if (bl == 0 && 8 * dg < D) acc8f(dsum + ((int64_t)bh * G.NS + row) * D + 8 * dg, acc, first);
+  if (bl == 0 && 8 * dg < D) acc8f(dsum + ((int64_t)bh * ns + row) * D + 8 * dg, acc, first);
 }
 
 static int tree_smem(const Plan& P) {
@@ -1390,6 +1393,15 @@ static int tree_smem(const Plan& P) {
   const int ch = chunk_cols((int)P.D);
   return kQueryTile * (ch + 4) * 4 + kQueryTile * (ch + 8) * P.esize + kQueryTile * S * 8 + kQueryTile * 4 +
          (S <= 8 ? kQueryTile * 8 * 20 : S <= 16 ? kQueryTile * 16 * 20 : 0);
+}
+
+static void launch_path_dsum(const float* dcp, float* dsum, const Geo& G, int D, int64_t BH, int first, int nr,
+                             int ns, hipStream_t st) {
+  const int64_t nrows = BH * G.NS;
+  const dim3 grid((unsigned)((nrows + 3) / 4));
+  if (D <= 32) hipLaunchKernelGGL(path_dsum_kernel<4>, grid, dim3(256), 0, st, dcp, dsum, G, D, nrows, first, nr, ns);
+  else if (D <= 64) hipLaunchKernelGGL(path_dsum_kernel<8>, grid, dim3(256), 0, st, dcp, dsum, G, D, nrows, first, nr, ns);
+  else hipLaunchKernelGGL(path_dsum_kernel<16>, grid, dim3(256), 0, st, dcp, dsum, G, D, nrows, first, nr, ns);
 }
 
 // dk from the summary gradient (and the leaf part): once per problem, after
@@ -1467,17 +1479,32 @@ static hipError_t tree_impl(const Plan& P, const void* q, const char* rec, void*
     a.dcp = (const float*)(ws + P.bws.dcp);
     const int64_t n8 = nqh * (D / 8);
     hipLaunchKernelGGL(dq_rows_kernel<E>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, a, n8);
-    const int64_t nrows = P.BH * P.geo.NS;
-    const dim3 grid((unsigned)((nrows + 3) / 4));
-    if (D <= 32) hipLaunchKernelGGL(path_dsum_kernel<4>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
-    else if (D <= 64) hipLaunchKernelGGL(path_dsum_kernel<8>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
-    else hipLaunchKernelGGL(path_dsum_kernel<16>, grid, dim3(256), 0, st, a.dcp, a.dsum, P.geo, D, nrows, a.first);
+    launch_path_dsum(a.dcp, a.dsum, P.geo, D, P.BH, a.first, P.geo.T * P.geo.b, P.geo.NS, st);
     return tree_adjoint<E>(P, a, chunk, st);
   }
   int pw2 = 1;
   while (pw2 < P.S) pw2 <<= 1;
   hipLaunchKernelGGL(slot_dlogp_kernel, dim3((unsigned)((nqh * pw2 + 255) / 256)), dim3(256), 0, st, a.slot_count,
                      a.slot_weight, a.delta, a.dl, (int)P.S, pw2, nqh, P.acc.mean);
+  if (P.leaf_path) {
+    // one-token leaves: the tree gradient along the paths per subtree of
+    // 2^g leaves, the root-path rows summed over the subtrees under each
+    // node, dq from the pairs' rows, then the key adjoint
+    hipError_t e = launch_leaf_path1(P, q, rec, ws, a.dsum, a.first, st);
+    if (e != hipSuccess) return e;
+    const int g = P.leaf_path;
+    if (P.geo.T > g) {
+      Geo top = P.geo;
+      top.T = P.geo.T - g;
+      top.NL = P.geo.NL >> g;
+      top.NS = P.geo.off[top.T + 1];
+      launch_path_dsum((const float*)(ws + P.bws.dcp), a.dsum, top, D, P.BH, a.first, leaf_path1_top_rows(), P.geo.NS,
+                       st);
+    }
+    const int64_t n8 = nqh * (D / 8);
+    hipLaunchKernelGGL(dq_rows_kernel<E>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, a, n8);
+    return tree_adjoint<E>(P, a, chunk, st);
+  }
   if (a.refc)
     hipLaunchKernelGGL(ref_causal_grad_kernel<E>, dim3((unsigned)((nqh + 255) / 256)), dim3(256), 0, st, a);
   // the band depths (before tree_dq_kernel, whose epilogue sums the pairs' dq rows)
