@@ -94,7 +94,8 @@ __global__ __launch_bounds__(256) void seg_sums_kernel(const float* __restrict__
 struct SumArgs {
   Geo geo;
   int H, D, mode;
-  int hilo_lam;         // levels 1 .. hilo_lam are read as MFMA tiles: hi, lo copies
+  int hilo_lam;         // levels 1 .. hilo_lam are read as MFMA tiles: hi copies
+  int lo_lam;           // levels 1 .. lo_lam also the lo copies (the sampler's float-accurate tiles)
   int t_lam;            // levels 1 .. t_lam also as the transposed copy
   const float* means;   // (BH, NL, D)
   const float* seg1;    // (BH, NL / kSeg, D) or null
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256) void summaries_kernel(SumArgs a) {
         tr[j] = (float)hi[j];
       }
       *(e8*)((E*)a.sum_hi + row_off) = hi;
-      *(e8*)((E*)a.sum_lo + row_off) = lo;
+      if (lam <= a.lo_lam) *(e8*)((E*)a.sum_lo + row_off) = lo;
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) tr[j] = val[j];
@@ -261,6 +262,7 @@ static hipError_t pool_impl(const Plan& P, const void* k, char* rec, hipStream_t
   a.hilo_lam = P.p.causal == TA_CAUSAL_EXACT || P.path_rows || P.leaf_path
                    ? G.T
                    : (P.sample_dense > P.tree_dense ? P.sample_dense : P.tree_dense);
+  a.lo_lam = P.p.causal == TA_CAUSAL_EXACT ? G.T : P.sample_dense;  // the backward reads hi only
   a.means = means;
   a.knodes = k;
   a.ksb = P.p.k_strides[0];
