@@ -75,8 +75,9 @@ typedef struct ta_problem {
                             tiles, wider ones per sampled path (0: the library's defaults,
                             which for 16-bit inputs with b = 2 or 4, leaf_block >= 2 and
                             T*b <= 32 take the backward's tree part along the sampled paths
-                            in the leaf backward); changes no result beyond rounding, for
-                            tuning and tests */
+                            in the leaf backward, and for 16-bit one-token binary leaves
+                            outside the reference causal mode per subtree of 64 leaves);
+                            changes no result beyond rounding, for tuning and tests */
   float scale;           /* leaf-block softmax scale */
   float max_logit;       /* child logits are clamped to +-max_logit/2 (binary compat trees:
                             the left/right logit to +-max_logit, _autograd.py:202) */

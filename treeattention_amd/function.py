@@ -59,8 +59,9 @@ class TreeOptions:
       evaluated as dense level tiles, wider ones per sampled path (0: the
       library's defaults, under which 16-bit inputs with b = 2 or 4,
       ``leaf_block >= 2`` and ``T*b <= 32`` take the backward's tree part
-      along the sampled paths inside the leaf backward); for tuning and
-      tests, results change only by rounding.
+      along the sampled paths inside the leaf backward, and 16-bit one-token
+      binary leaves outside the reference causal mode per subtree of 64
+      leaves); for tuning and tests, results change only by rounding.
     """
 
     num_samples: int
