@@ -92,7 +92,7 @@ struct LogitPipe {
     if (w < ntiles) load(hi, lo, row(w), lane, ah, al);
   }
 
-  template <class RowFn>
+  template <int kStride, class RowFn>
   __device__ __forceinline__ void run(const RowFrags<E, D> (&qa)[4], float* Xs, const E* hi, const E* lo, RowFn row,
                                       int ntiles, int lane, int w) {
     const int col = lane & 15, g = lane >> 4;
@@ -107,7 +107,7 @@ struct LogitPipe {
           c = M::mma(ah[ks], qa[qt].f[ks], c);
           if constexpr (kLo) c = M::mma(al[ks], qa[qt].f[ks], c);
         }
-        *(f32x4*)(Xs + (16 * qt + col) * kXS + 16 * ct + 4 * g) = c;
+        *(f32x4*)(Xs + (16 * qt + col) * kStride + 16 * ct + 4 * g) = c;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -139,7 +139,7 @@ struct Passes {
     if (causal) n = min(n, ((blk_hi >> (lb * (T - d))) + 1) << lb);
     return n;
   }
-  __device__ __forceinline__ int nbatch() const { return (nbt + kLevelCols / 16 - 1) / (kLevelCols / 16); }
+  __device__ __forceinline__ int nbatch(int cols) const { return (nbt + cols / 16 - 1) / (cols / 16); }
   // summary row of global boundary tile t
   __device__ __forceinline__ int64_t brow(int t) const {
     int d = 0, t0 = 0;
@@ -600,7 +600,7 @@ struct Walk {
 // kB: branching known at compile time (2 or 4), or 0 for the runtime value.
 // kNI: (query, sample) items per thread, >= 64 * S / 256.
 // kReplay: decisions come from a.paths (packed path bits) instead of Gumbel-max.
-template <typename E, int D, int kB, int kNI, bool kReplay>
+template <typename E, int D, int kB, int kNI, bool kReplay, int kC>
 // Binary trees with 16 items per thread at head dims of 96 and up spill at
 // two waves per SIMD; one wave with the whole register file runs them faster
 // (the reference tree at L = 16384, 64 paths: 5.85 -> 4.14 ms; branching 4
@@ -617,8 +617,8 @@ __global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) voi
   const int64_t rows = G.NS;
   constexpr bool kLo = sizeof(E) == 2;
 
-  float* Xs = (float*)smem;                      // [64][kXS] logits of one level pass
-  float* logA = Xs + kQueryTile * kXS;           // [64][T+1] causal boundary log-mass
+  float* Xs = (float*)smem;                      // [64][(kC + 4)] logits of one level pass
+  float* logA = Xs + kQueryTile * (kC + 4);           // [64][T+1] causal boundary log-mass
   float* xb = logA + kQueryTile * (T + 1);       // [64][T*b] boundary child logits
   // after the walk Xs is reused by finish()
 
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) voi
   ps.nbt = 0;
   if (ps.causal)
     for (int d = 0; d < T; ++d) ps.nbt += ps.btiles(d);
-  const int nbatch = ps.causal ? ps.nbatch() : 0;
+  const int nbatch = ps.causal ? ps.nbatch(kC) : 0;
 
   Walk<kB, kNI, kReplay> wk;
   wk.init(a, l0, nq, bb, h, tid);
@@ -653,41 +653,41 @@ __global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) voi
   LogitPipe<E, D, kLo> pipe;
   pipe.rmax = ps.base + rows - 1;
   auto tiles_of = [&](int p, int d, int c0) {
-    if (p < nbatch) return min(kLevelCols / 16, ps.nbt - p * (kLevelCols / 16));
-    return (min(kLevelCols, ps.level_cols(d) - c0) + 15) >> 4;
+    if (p < nbatch) return min(kC / 16, ps.nbt - p * (kC / 16));
+    return (min(kC, ps.level_cols(d) - c0) + 15) >> 4;
   };
   auto prefetch = [&](int p, int d, int c0) {
     if (p < nbatch) {
-      const int t0 = p * (kLevelCols / 16);
+      const int t0 = p * (kC / 16);
       pipe.prefetch(hi, lo, [&](int t) { return ps.brow(t0 + t); }, tiles_of(p, d, c0), lane, w);
     } else {
       const int64_t r0 = ps.base + G.off[d + 1] + c0;
       pipe.prefetch(hi, lo, [&](int t) { return r0 + 16 * t; }, tiles_of(p, d, c0), lane, w);
     }
   };
-  // A level wider than kLevelCols children takes several passes, run from the
+  // A level wider than kC children takes several passes, run from the
   // highest column chunk down: an item that moves in the pass at c0 lands on a
   // node >= c0 of the next depth, whose children (>= 2 c0) lie past every
   // later pass of the level, so no item decides twice in one level.
-  auto last_c0 = [&](int dd) { return (ps.level_cols(dd) - 1) / kLevelCols * kLevelCols; };
+  auto last_c0 = [&](int dd) { return (ps.level_cols(dd) - 1) / kC * kC; };
   const int Td = a.Td;  // dense levels 0 .. Td - 1
-  int p = 0, d = 0, c0 = 0;  // current pass (level 0 has b <= kLevelCols children)
+  int p = 0, d = 0, c0 = 0;  // current pass (level 0 has b <= kC children)
   if (nbatch > 0 || Td > 0) prefetch(0, 0, 0);
   while (p < nbatch || d < Td) {
     const int nt = tiles_of(p, d, c0);
     if (p < nbatch) {
-      const int t0 = p * (kLevelCols / 16);
-      pipe.run(qa, Xs, hi, lo, [&](int t) { return ps.brow(t0 + t); }, nt, lane, w);
+      const int t0 = p * (kC / 16);
+      pipe.template run<kC + 4>(qa, Xs, hi, lo, [&](int t) { return ps.brow(t0 + t); }, nt, lane, w);
     } else {
       const int64_t r0 = ps.base + G.off[d + 1] + c0;
-      pipe.run(qa, Xs, hi, lo, [&](int t) { return r0 + 16 * t; }, nt, lane, w);
+      pipe.template run<kC + 4>(qa, Xs, hi, lo, [&](int t) { return r0 + 16 * t; }, nt, lane, w);
     }
     __syncthreads();
     // next pass, and its first tile in flight while this one is consumed
     int np = p + 1, nd = d, nc0 = c0;
     if (p >= nbatch) {
       if (c0 > 0) {
-        nc0 = c0 - kLevelCols;
+        nc0 = c0 - kC;
       } else {
         ++nd;
         nc0 = nd < Td ? last_c0(nd) : 0;
@@ -704,9 +704,9 @@ __global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) voi
         int t0 = 0;
         for (int dd = 0; dd < T; ++dd) {
           // column of the query's boundary node's first child in the global tile space
-          const int gc = 16 * t0 + ((blk >> (lb * (T - dd))) << lb) - ps.bc0(dd) - p * kLevelCols;
-          if ((dd & 3) == w && gc >= 0 && gc < kLevelCols)
-            for (int j = 0; j < b; ++j) xb[qb * T * b + dd * b + j] = clampf(Xs[qb * kXS + gc + j], a.maxhalf);
+          const int gc = 16 * t0 + ((blk >> (lb * (T - dd))) << lb) - ps.bc0(dd) - p * kC;
+          if ((dd & 3) == w && gc >= 0 && gc < kC)
+            for (int j = 0; j < b; ++j) xb[qb * T * b + dd * b + j] = clampf(Xs[qb * (kC + 4) + gc + j], a.maxhalf);
           t0 += ps.btiles(dd);
         }
       }
@@ -753,14 +753,14 @@ __global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) voi
         }
       }
     } else {
-      const int ncols = min(kLevelCols, ps.level_cols(d) - c0);
+      const int ncols = min(kC, ps.level_cols(d) - c0);
 #pragma unroll
       for (int k = 0; k < kNI; ++k) {
         const int qi = wk.iq(k);
         if (qi >= kQueryTile) continue;
         const int base = (wk.node[k] << lb) - c0;
         if (base < 0 || base >= ncols) continue;
-        wk.decide(a, logA, k, d, Xs + qi * kXS + base);
+        wk.decide(a, logA, k, d, Xs + qi * (kC + 4) + base);
       }
     }
     __syncthreads();
@@ -873,9 +873,17 @@ __global__ __launch_bounds__(256) void sample_sparse_kernel(SampleArgs a) {
 
 // Xs (which the final phase's three [64][S] arrays alias: 3 * 64 * 64 * 4
 // bytes < sizeof Xs), logA and the boundary child logits.
-static inline int sample_smem(const Plan& P) {
+static inline int sample_smem(const Plan& P, int cols) {
   const int T = P.geo.T, b = P.geo.b;
-  return kQueryTile * kXS * 4 + kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
+  return kQueryTile * (cols + 4) * 4 + kQueryTile * (T + 1) * 4 + kQueryTile * T * b * 4;
+}
+
+// Child columns per level pass of sample_kernel: 128 where that lets a third
+// workgroup onto a CU (head dim 32, whose registers allow three waves per
+// SIMD; up to 16 samples, whose final phase fits the smaller logit tile),
+// else kLevelCols.
+static inline int sample_cols(const Plan& P) {
+  return P.D <= 32 && P.S <= 16 && (P.geo.b == 2 || P.geo.b == 4) ? 128 : kLevelCols;
 }
 
 template <bool kReplay, typename E, int D, int kB, int kNI>
@@ -916,16 +924,22 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
   a.Td = P.sample_dense;
   a.pair_rows = P.p.tree_mode != TA_TREE_NATURAL && P.geo.b == 2;
   a.logA = (float*)(rec + P.rec.logA);
-  const int smem = sample_smem(P);
-  auto launch = [&](auto kern) -> hipError_t {
+  auto launch = [&](auto kern, int smem) -> hipError_t {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3((unsigned)((P.L + kQueryTile - 1) / kQueryTile), P.BH), dim3(256), smem, st, a);
     return hipGetLastError();
   };
-  hipError_t e = launch(sample_kernel<E, D, kB, kNI, kReplay>);
+  hipError_t e;
+  if constexpr ((kB == 2 || kB == 4) && D <= 32 && kNI == 4) {
+    e = sample_cols(P) == 128 ? launch(sample_kernel<E, D, kB, kNI, kReplay, 128>, sample_smem(P, 128))
+                              : launch(sample_kernel<E, D, kB, kNI, kReplay, kLevelCols>, sample_smem(P, kLevelCols));
+  } else {
+    e = launch(sample_kernel<E, D, kB, kNI, kReplay, kLevelCols>, sample_smem(P, kLevelCols));
+  }
   if constexpr (kB == 2 || kB == 4)
-    if (e == hipSuccess && P.sample_dense < P.geo.T) e = launch(sample_sparse_kernel<E, D, kB, kNI, kReplay>);
+    if (e == hipSuccess && P.sample_dense < P.geo.T)
+      e = launch(sample_sparse_kernel<E, D, kB, kNI, kReplay>, sample_smem(P, kLevelCols));
   return e;
 }
 
