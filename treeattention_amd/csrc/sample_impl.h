@@ -605,7 +605,7 @@ template <typename E, int D, int kB, int kNI, bool kReplay, int kC>
 // two waves per SIMD; one wave with the whole register file runs them faster
 // (the reference tree at L = 16384, 64 paths: 5.85 -> 4.14 ms; branching 4
 // is faster at two waves).
-__global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : 2) void sample_kernel(SampleArgs a) {
+__global__ __launch_bounds__(256, (kB == 2 && kNI >= 16 && D >= 96) ? 1 : kC < kLevelCols ? 3 : 2) void sample_kernel(SampleArgs a) {
   extern __shared__ __align__(16) char smem[];
   const Geo& G = a.geo;
   const int bh = blockIdx.y, bb = bh / a.H, h = bh - bb * a.H;
@@ -879,11 +879,12 @@ static inline int sample_smem(const Plan& P, int cols) {
 }
 
 // Child columns per level pass of sample_kernel: 128 where that lets a third
-// workgroup onto a CU (head dim 32, whose registers allow three waves per
-// SIMD; up to 16 samples, whose final phase fits the smaller logit tile),
-// else kLevelCols.
+// workgroup onto a CU (head dims up to 32, or 64 for 16-bit inputs, whose
+// registers fit three waves per SIMD; up to 16 samples, whose final phase fits
+// the smaller logit tile), else kLevelCols.
 static inline int sample_cols(const Plan& P) {
-  return P.D <= 32 && P.S <= 16 && (P.geo.b == 2 || P.geo.b == 4) ? 128 : kLevelCols;
+  return (P.D <= 32 || (P.D <= 64 && P.esize == 2)) && P.S <= 16 && (P.geo.b == 2 || P.geo.b == 4) ? 128
+                                                                                                   : kLevelCols;
 }
 
 template <bool kReplay, typename E, int D, int kB, int kNI>
@@ -931,7 +932,7 @@ static hipError_t sample_impl(const Plan& P, const void* q, const float* U, uint
     return hipGetLastError();
   };
   hipError_t e;
-  if constexpr ((kB == 2 || kB == 4) && D <= 32 && kNI == 4) {
+  if constexpr ((kB == 2 || kB == 4) && (D <= 32 || (D <= 64 && sizeof(E) == 2)) && kNI == 4) {
     e = sample_cols(P) == 128 ? launch(sample_kernel<E, D, kB, kNI, kReplay, 128>, sample_smem(P, 128))
                               : launch(sample_kernel<E, D, kB, kNI, kReplay, kLevelCols>, sample_smem(P, kLevelCols));
   } else {
