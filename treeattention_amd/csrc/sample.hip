@@ -11,4 +11,6 @@ hipError_t launch_sample(const Plan& P, const void* q, const float* U, uint64_t 
   return sample_dispatch<false>(P, q, U, seed, weights, rec, st, nullptr);
 }
 
+TA_SAMPLE_TYPED(false, bf16)
+
 }  // namespace ta

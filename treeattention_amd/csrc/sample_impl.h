@@ -974,16 +974,40 @@ static hipError_t sample_d(const Plan& P, const void* q, const float* U, uint64_
   }
 }
 
-// The sampler for every supported element type, head dim and branching, with
-// Gumbel-max decisions (kReplay false) or replayed paths (kReplay true).
+// The sampler of one element type, every head dim and branching, with
+// Gumbel-max decisions (kReplay false) or replayed paths (kReplay true); each
+// (kReplay, E) is defined in a translation unit of its own (sample*.hip), so
+// the six compile in parallel.
+template <bool kReplay, typename E>
+hipError_t sample_typed(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights, char* rec,
+                        hipStream_t st, const uint8_t* paths);
+#define TA_SAMPLE_TYPED_DECL(R, E)                                                                             \
+  template <>                                                                                                  \
+  hipError_t sample_typed<R, E>(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights, \
+                                char* rec, hipStream_t st, const uint8_t* paths);
+TA_SAMPLE_TYPED_DECL(false, float)
+TA_SAMPLE_TYPED_DECL(false, bf16)
+TA_SAMPLE_TYPED_DECL(false, f16)
+TA_SAMPLE_TYPED_DECL(true, float)
+TA_SAMPLE_TYPED_DECL(true, bf16)
+TA_SAMPLE_TYPED_DECL(true, f16)
+#undef TA_SAMPLE_TYPED_DECL
+
 template <bool kReplay>
 static hipError_t sample_dispatch(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,
                                   char* rec, hipStream_t st, const uint8_t* paths) {
   switch (P.p.dtype) {
-    case TA_F32: return sample_d<kReplay, float>(P, q, U, seed, weights, rec, st, paths);
-    case TA_BF16: return sample_d<kReplay, bf16>(P, q, U, seed, weights, rec, st, paths);
-    default: return sample_d<kReplay, f16>(P, q, U, seed, weights, rec, st, paths);
+    case TA_F32: return sample_typed<kReplay, float>(P, q, U, seed, weights, rec, st, paths);
+    case TA_BF16: return sample_typed<kReplay, bf16>(P, q, U, seed, weights, rec, st, paths);
+    default: return sample_typed<kReplay, f16>(P, q, U, seed, weights, rec, st, paths);
   }
 }
+
+#define TA_SAMPLE_TYPED(R, E)                                                                                    \
+  template <>                                                                                                    \
+  hipError_t sample_typed<R, E>(const Plan& P, const void* q, const float* U, uint64_t seed, float* weights,   \
+                                char* rec, hipStream_t st, const uint8_t* paths) {                              \
+    return sample_d<R, E>(P, q, U, seed, weights, rec, st, paths);                                               \
+  }
 
 }  // namespace ta

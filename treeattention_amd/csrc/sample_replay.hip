@@ -9,4 +9,6 @@ hipError_t launch_sample_replay(const Plan& P, const void* q, float* weights, ch
   return sample_dispatch<true>(P, q, nullptr, 0, weights, rec, st, paths);
 }
 
+TA_SAMPLE_TYPED(true, bf16)
+
 }  // namespace ta
